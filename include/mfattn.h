@@ -1,0 +1,133 @@
+/* mfattn: MI355X (gfx950) packed-sequence attention -- C ABI.
+ *
+ * Plain C declarations: device pointers, sizes, an opaque HIP stream.  No
+ * allocation happens inside any entry point; callers pass every buffer,
+ * including the plan and workspace whose sizes the *_bytes queries return.
+ * Every entry point is stream-ordered on `stream` (a hipStream_t, NULL =
+ * default stream), never synchronises the host, and keeps no mutable global
+ * state, so it is safe to call from several host threads.
+ *
+ * Status: 0 on success, a negative MF_ERR_* code otherwise; the message of
+ * the calling thread's last failure is returned by mf_last_error().
+ *
+ * Tensor layouts (row-major, last dimension fastest):
+ *   query    [B, T, Hq, D]     key/value [B, S, Hkv, D]     (BTHD)
+ *   out      [B, T, Hq, D]     lse       [B, Hq, T] fp32 (natural log;
+ *                                         +inf for rows with no valid key)
+ *   segment_ids [B, T] int32 (0 = padding); mask [B, T] (or [B, S] in
+ *   MF_MODE_KEYMASK_BIDIR) int32 or uint8/bool.
+ * Query head h reads KV head h / (Hq / Hkv).
+ */
+#ifndef MFATTN_H
+#define MFATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define MF_OK 0
+#define MF_ERR_INVALID_ARGUMENT (-1) /* null pointer, non-positive size   */
+#define MF_ERR_SHAPE (-2)            /* query/KV shapes incompatible      */
+#define MF_ERR_HEADS (-3)            /* Hq not divisible by Hkv           */
+#define MF_ERR_HEAD_DIM (-4)         /* head_dim other than 64            */
+#define MF_ERR_DTYPE (-5)            /* unknown dtype / mask dtype        */
+#define MF_ERR_MODE (-6)             /* unknown mask mode                 */
+#define MF_ERR_WORKSPACE (-7)        /* plan/workspace smaller than needed */
+#define MF_ERR_HIP (-9)              /* a HIP launch failed               */
+
+/* element types of query/key/value/out (and gradients) */
+#define MF_DTYPE_F32 0
+#define MF_DTYPE_BF16 1
+
+/* mask element types */
+#define MF_MASK_I32 0
+#define MF_MASK_U8 1
+
+/* mask semantics */
+#define MF_MODE_PACKED_CAUSAL 0 /* kernels/attention.py:79-108, :245-261     */
+#define MF_MODE_PACKED_BIDIR 1  /* kernels/bidirectional.py:24-31 (with ids) */
+#define MF_MODE_KEYMASK_BIDIR 2 /* kernels/bidirectional.py:21-23 (no ids)   */
+
+/* tile classes stored in the plan's tile map */
+#define MF_TILE_EMPTY 0
+#define MF_TILE_PARTIAL 1
+#define MF_TILE_FULL 2
+
+/* tile edge (queries and keys) of the block map */
+#define MF_TILE 128
+
+/* Offsets (bytes) of the plan's sections, for callers that inspect it:
+ * [0] qid int32 [B][nQ*128]   canonical query ids (-1 = inactive)
+ * [1] kid int32 [B][nK*128]   canonical key ids   (-2 = inactive)
+ * [2] tile map uint8 [B][nQ][nK]
+ * [3] q_count int32 [B][nQ]    [4] q_list int32 [B][nQ][nK] (kj*4 + class)
+ * [5] k_count int32 [B][nK]    [6] k_list int32 [B][nK][nQ] (qi*4 + class)
+ * [7] run scratch              [8] total size
+ * with nQ = ceil(T/128), nK = ceil(S/128). */
+void mf_plan_layout(int batch, int q_len, int kv_len, size_t offsets[9]);
+size_t mf_plan_bytes(int batch, int q_len, int kv_len);
+
+/* Block-mask builder.  Replaces the dense validity grids of
+ * kernels/attention.py:79-108 (_packed_valid_mask) and
+ * kernels/bidirectional.py:21-31 with a per-(row, 128-query tile, 128-key
+ * tile) EMPTY/PARTIAL/FULL map plus compacted per-tile work lists.
+ * segment_ids may be NULL only in MF_MODE_KEYMASK_BIDIR; there `mask` is the
+ * [B, kv_len] key mask and q_len may differ from kv_len.  In the packed
+ * modes q_len must equal kv_len. */
+int mf_block_map(const int32_t* segment_ids, const void* mask, int mask_dtype,
+                 int mode, int batch, int q_len, int kv_len, void* plan,
+                 size_t plan_bytes, void* stream);
+
+/* Forward.  Replaces _dense_attention with its callers
+ * dense_packed_causal_attention (kernels/attention.py:245-261, mode 0) and
+ * bidirectional.attention (kernels/bidirectional.py:7-35, modes 1 and 2).
+ * Rows with no valid key (inactive queries) are written as exact zeros.
+ * `scale` multiplies the logits (the reference uses head_dim ** -0.5,
+ * attention.py:23-25).  `plan` must come from mf_block_map with the same
+ * batch/q_len/kv_len and the mode the caller intends. */
+int mf_attn_fwd(const void* q, const void* k, const void* v, int dtype,
+                int batch, int q_len, int kv_len, int q_heads, int kv_heads,
+                int head_dim, int mode, float scale, const void* plan,
+                size_t plan_bytes, void* out, float* lse, void* stream);
+
+/* Backward of mf_attn_fwd (the JAX-autodiff VJP the reference relies on):
+ * dq, dk, dv in the element type of q/k/v; dk/dv summed over each GQA group.
+ * `workspace` holds the per-row rowsum(dO * O) (mf_attn_bwd_workspace_bytes).
+ * Deterministic: no atomics, fixed reduction order. */
+size_t mf_attn_bwd_workspace_bytes(int batch, int q_len, int q_heads);
+int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                const void* dout, const float* lse, int dtype, int batch,
+                int q_len, int kv_len, int q_heads, int kv_heads, int head_dim,
+                int mode, float scale, const void* plan, size_t plan_bytes,
+                void* dq, void* dk, void* dv, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* Ragged KV-cached decode.  Replaces dense_cached_attention
+ * (kernels/attention.py:264-282) / cudnn_cached_attention (:366-396): one
+ * query token per row attends to cache slots [0, lengths[b]) of a
+ * [B, capacity, Hkv, D] cache.  lengths[b] > capacity reads the whole cache;
+ * lengths[b] <= 0 reproduces the reference's unguarded result (a uniform
+ * average over all `capacity` slots).  Split-K over the cache with a
+ * log-sum-exp merge; `workspace` holds the partials. */
+size_t mf_decode_workspace_bytes(int batch, int capacity, int q_heads,
+                                 int head_dim);
+int mf_decode(const void* q, const void* k_cache, const void* v_cache,
+              const int32_t* lengths, int dtype, int batch, int capacity,
+              int q_heads, int kv_heads, int head_dim, float scale, void* out,
+              void* workspace, size_t workspace_bytes, void* stream);
+
+/* Message of the calling thread's most recent failure ("" if none). */
+const char* mf_last_error(void);
+
+/* Library version string. */
+const char* mf_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MFATTN_H */

@@ -1,0 +1,199 @@
+// C ABI of the mfattn library: argument validation, error reporting and the
+// launches.  Every check here runs on the host before anything is enqueued,
+// so a malformed call returns an MF_ERR_* code (and leaves a message for
+// mf_last_error) without touching the GPU.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/mfattn.h"
+#include "mf_common.h"
+
+namespace mf {
+hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, int mode, int batch,
+                            int q_len, int kv_len, void* plan, hipStream_t stream);
+hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32, int batch, int T,
+                           int S, int Hq, int Hkv, int mode, float scale, const void* plan,
+                           void* out, float* lse, hipStream_t stream);
+hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                           const void* dout, const float* lse, bool f32, int batch, int T, int S,
+                           int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
+                           void* dk, void* dv, float* delta, hipStream_t stream);
+size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk);
+int decode_chunk(bool f32);
+hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
+                         bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
+                         void* workspace, hipStream_t stream);
+}  // namespace mf
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return MF_OK;
+}
+
+int check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(MF_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+int check_mode(int mode) {
+  if (mode != MF_MODE_PACKED_CAUSAL && mode != MF_MODE_PACKED_BIDIR && mode != MF_MODE_KEYMASK_BIDIR)
+    return fail(MF_ERR_MODE, "Unknown mask mode %d", mode);
+  return MF_OK;
+}
+
+// Shape checks shared by forward and backward.
+int check_attn(int dtype, int batch, int q_len, int kv_len, int q_heads, int kv_heads,
+               int head_dim, int mode, size_t plan_bytes) {
+  if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
+  if (int rc = check_mode(mode)) return rc;
+  if (batch < 1 || q_len < 1 || kv_len < 1 || q_heads < 1 || kv_heads < 1)
+    return fail(MF_ERR_INVALID_ARGUMENT,
+                "Sizes must be positive (batch=%d q_len=%d kv_len=%d q_heads=%d kv_heads=%d)",
+                batch, q_len, kv_len, q_heads, kv_heads);
+  if (mode != MF_MODE_KEYMASK_BIDIR && q_len != kv_len)
+    return fail(MF_ERR_SHAPE, "Packed attention query/KV shapes are incompatible");
+  if (q_heads % kv_heads) return fail(MF_ERR_HEADS, "Query heads must be divisible by KV heads");
+  if (head_dim != mf::kD)
+    return fail(MF_ERR_HEAD_DIM, "head_dim %d is not supported (kernels serve head_dim 64)", head_dim);
+  const size_t need = mf::plan_layout(batch, q_len, kv_len).total;
+  if (plan_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "plan holds %zu bytes, %zu needed", plan_bytes, need);
+  return MF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void mf_plan_layout(int batch, int q_len, int kv_len, size_t offsets[9]) {
+  const mf::PlanLayout p = mf::plan_layout(batch, q_len, kv_len);
+  offsets[0] = p.qid;
+  offsets[1] = p.kid;
+  offsets[2] = p.tmap;
+  offsets[3] = p.qcnt;
+  offsets[4] = p.qlist;
+  offsets[5] = p.kcnt;
+  offsets[6] = p.klist;
+  offsets[7] = p.runs;
+  offsets[8] = p.total;
+}
+
+size_t mf_plan_bytes(int batch, int q_len, int kv_len) {
+  if (batch < 1 || q_len < 1 || kv_len < 1) return 0;
+  return mf::plan_layout(batch, q_len, kv_len).total;
+}
+
+int mf_block_map(const int32_t* segment_ids, const void* mask, int mask_dtype, int mode, int batch,
+                 int q_len, int kv_len, void* plan, size_t plan_bytes, void* stream) {
+  if (int rc = check_mode(mode)) return rc;
+  if (mask_dtype != MF_MASK_I32 && mask_dtype != MF_MASK_U8)
+    return fail(MF_ERR_DTYPE, "Unsupported mask dtype code %d", mask_dtype);
+  if (batch < 1 || q_len < 1 || kv_len < 1)
+    return fail(MF_ERR_INVALID_ARGUMENT, "Sizes must be positive (batch=%d q_len=%d kv_len=%d)",
+                batch, q_len, kv_len);
+  if (mode != MF_MODE_KEYMASK_BIDIR) {
+    if (q_len != kv_len)
+      return fail(MF_ERR_SHAPE, "Packed attention query/KV shapes are incompatible");
+    if (!segment_ids) return fail(MF_ERR_INVALID_ARGUMENT, "segment_ids is required in packed modes");
+  }
+  if (!mask || !plan) return fail(MF_ERR_INVALID_ARGUMENT, "mask and plan must be non-null");
+  const size_t need = mf::plan_layout(batch, q_len, kv_len).total;
+  if (plan_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "plan holds %zu bytes, %zu needed", plan_bytes, need);
+  return check_hip(mf::launch_block_map(segment_ids, mask, mask_dtype == MF_MASK_U8, mode, batch,
+                                        q_len, kv_len, plan, static_cast<hipStream_t>(stream)),
+                   "mf_block_map launch");
+}
+
+int mf_attn_fwd(const void* q, const void* k, const void* v, int dtype, int batch, int q_len,
+                int kv_len, int q_heads, int kv_heads, int head_dim, int mode, float scale,
+                const void* plan, size_t plan_bytes, void* out, float* lse, void* stream) {
+  if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
+    return rc;
+  if (!q || !k || !v || !plan || !out || !lse)
+    return fail(MF_ERR_INVALID_ARGUMENT, "q, k, v, plan, out and lse must be non-null");
+  return check_hip(mf::launch_attn_fwd(q, k, v, dtype == MF_DTYPE_F32, batch, q_len, kv_len,
+                                       q_heads, kv_heads, mode, scale, plan, out, lse,
+                                       static_cast<hipStream_t>(stream)),
+                   "mf_attn_fwd launch");
+}
+
+size_t mf_attn_bwd_workspace_bytes(int batch, int q_len, int q_heads) {
+  if (batch < 1 || q_len < 1 || q_heads < 1) return 0;
+  return sizeof(float) * (size_t)batch * q_len * q_heads;
+}
+
+int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                const float* lse, int dtype, int batch, int q_len, int kv_len, int q_heads,
+                int kv_heads, int head_dim, int mode, float scale, const void* plan,
+                size_t plan_bytes, void* dq, void* dk, void* dv, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
+    return rc;
+  if (!q || !k || !v || !out || !dout || !lse || !plan || !dq || !dk || !dv || !workspace)
+    return fail(MF_ERR_INVALID_ARGUMENT, "every tensor pointer and the workspace must be non-null");
+  const size_t need = mf_attn_bwd_workspace_bytes(batch, q_len, q_heads);
+  if (workspace_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  return check_hip(mf::launch_attn_bwd(q, k, v, out, dout, lse, dtype == MF_DTYPE_F32, batch, q_len,
+                                       kv_len, q_heads, kv_heads, mode, scale, plan, dq, dk, dv,
+                                       static_cast<float*>(workspace),
+                                       static_cast<hipStream_t>(stream)),
+                   "mf_attn_bwd launch");
+}
+
+size_t mf_decode_workspace_bytes(int batch, int capacity, int q_heads, int head_dim) {
+  if (batch < 1 || capacity < 1 || q_heads < 1 || head_dim != mf::kD) return 0;
+  // bf16 uses the smaller chunk count; size for the fp32 chunk (the larger one)
+  return mf::decode_workspace_bytes(batch, capacity, q_heads, mf::decode_chunk(true));
+}
+
+int mf_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* lengths,
+              int dtype, int batch, int capacity, int q_heads, int kv_heads, int head_dim,
+              float scale, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
+  if (batch < 1 || capacity < 1 || q_heads < 1 || kv_heads < 1)
+    return fail(MF_ERR_INVALID_ARGUMENT,
+                "Sizes must be positive (batch=%d capacity=%d q_heads=%d kv_heads=%d)", batch,
+                capacity, q_heads, kv_heads);
+  if (head_dim != mf::kD)
+    return fail(MF_ERR_SHAPE, "Cached attention query/KV shapes are incompatible");
+  if (q_heads % kv_heads) return fail(MF_ERR_HEADS, "Query heads must be divisible by KV heads");
+  if (q_heads / kv_heads > 8)
+    return fail(MF_ERR_HEADS, "Decode serves at most 8 query heads per KV head (got %d)",
+                q_heads / kv_heads);
+  if (!q || !k_cache || !v_cache || !lengths || !out || !workspace)
+    return fail(MF_ERR_INVALID_ARGUMENT, "every tensor pointer and the workspace must be non-null");
+  const size_t need = mf_decode_workspace_bytes(batch, capacity, q_heads, head_dim);
+  if (workspace_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  return check_hip(mf::launch_decode(q, k_cache, v_cache, lengths, dtype == MF_DTYPE_F32, batch,
+                                     capacity, q_heads, kv_heads, scale, out, workspace,
+                                     static_cast<hipStream_t>(stream)),
+                   "mf_decode launch");
+}
+
+const char* mf_last_error(void) { return g_last_error.c_str(); }
+
+const char* mf_version(void) { return "mfattn 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,736 @@
+// Backward of the segment-masked flash forward on gfx950.
+//
+// Three deterministic launches (no atomics, fixed reduction order):
+//   1. delta:  D[b,h,t] = sum_d dO * O   (fp32), one thread per (b, t, h).
+//   2. dq:     per 128-query tile (like the forward): recompute
+//              S^T = K Q^T and dP^T = V dO^T over the tile's non-empty key
+//              tiles, P^T = exp2(c S^T - lse2), dS^T = P^T (dP^T - D), and
+//              dQ^T += K^T dS^T.  K^T is staged k-permuted in LDS so dS^T is
+//              fed from its accumulator registers as the B operand.
+//   3. dkdv:   per 128-key tile and KV head: K and V stay in registers;
+//              for every non-empty query tile and every query head of the
+//              GQA group, S = Q K^T and dP = dO V^T (accumulator column =
+//              key), then dV^T += dO^T P and dK^T += Q^T dS with Q^T and
+//              dO^T staged k-permuted in LDS.  The group's heads are summed
+//              in registers, which is the transpose of the reference's
+//              jnp.repeat of K/V (kernels/attention.py:19-22).
+// Rows with no valid key have lse = +inf, so their P is exactly 0 and they
+// contribute nothing; their dq is written as 0.
+#include <type_traits>
+
+#include "mf_common.h"
+
+namespace mf {
+
+struct BwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const void* dout;
+  const float* lse;
+  float* delta;
+  void* dq;
+  void* dk;
+  void* dv;
+  const int* qid;
+  const int* kid;
+  const int* qcnt;
+  const int* qlist;
+  const int* kcnt;
+  const int* klist;
+  int T, S, Hq, Hkv, G, hchunks;
+  int nq, nk, tq_pad, tk_pad;
+  int causal;
+  float scale, scale_log2;
+};
+
+constexpr int kStep = 64;
+constexpr int kRow = kD + 8;   // bf16 LDS row pitch (144 B)
+constexpr int kRowF = kD + 1;  // fp32 LDS row pitch
+
+// ---------------------------------------------------------------------------
+// 1. delta
+// ---------------------------------------------------------------------------
+template <bool F32>
+__global__ __launch_bounds__(256) void bwd_delta_kernel(BwdArgs a, int B) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // (b, t, h)
+  const size_t total = (size_t)B * a.T * a.Hq;
+  if (idx >= total) return;
+  const int h = idx % a.Hq;
+  const size_t bt = idx / a.Hq;
+  const int t = bt % a.T;
+  const int b = bt / a.T;
+  float acc = 0.f;
+  if constexpr (!F32) {
+    const bf16* o = reinterpret_cast<const bf16*>(a.out) + idx * kD;
+    const bf16* g = reinterpret_cast<const bf16*>(a.dout) + idx * kD;
+#pragma unroll
+    for (int c8 = 0; c8 < 8; ++c8) {
+      const bf16x8 x = ld_bf16x8(o + c8 * 8);
+      const bf16x8 y = ld_bf16x8(g + c8 * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf((float)x[e], (float)y[e], acc);
+    }
+  } else {
+    const float* o = reinterpret_cast<const float*>(a.out) + idx * kD;
+    const float* g = reinterpret_cast<const float*>(a.dout) + idx * kD;
+#pragma unroll
+    for (int c4 = 0; c4 < 16; ++c4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(o + c4 * 4);
+      const f32x4 y = *reinterpret_cast<const f32x4*>(g + c4 * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fmaf(x[e], y[e], acc);
+    }
+  }
+  a.delta[((size_t)b * a.Hq + h) * a.T + t] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// 2. dq (per query tile)
+// ---------------------------------------------------------------------------
+template <bool F32>
+struct DqLds;
+
+template <>
+struct DqLds<false> {
+  bf16 k[2][kStep * kRow];   // K   [key][d]
+  bf16 v[2][kStep * kRow];   // V   [key][d]
+  bf16 kt[2][kD * kRow];     // K^T [d][key, k-permuted]
+  int kid[2][kStep];
+};
+
+template <>
+struct DqLds<true> {
+  float k[2][kStep * kRowF];
+  float v[2][kStep * kRowF];
+  int kid[2][kStep];
+};
+
+template <bool F32>
+struct DqStage {
+  u32x4 r[F32 ? 8 : 4];
+};
+
+template <bool F32>
+__device__ __forceinline__ void dq_load(const BwdArgs& a, int b, int kvh, int kb, DqStage<F32>& st) {
+  const int tid = threadIdx.x;
+  if constexpr (!F32) {
+    // threads 0..127: K, 4 consecutive keys x one d chunk (natural + transposed)
+    // threads 128..255: V, 4 consecutive keys x one d chunk (natural)
+    const bf16* src = reinterpret_cast<const bf16*>(tid < 128 ? a.k : a.v);
+    const int u = tid & 127;
+    const int kg = u >> 3, ch = u & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kb + kg * 4 + i;
+      st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
+                          : u32x4{0, 0, 0, 0};
+    }
+  } else {
+    const float* ks = reinterpret_cast<const float*>(a.k);
+    const float* vs = reinterpret_cast<const float*>(a.v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + 256 * i;
+      const int key = kb + (u >> 4), ch = u & 15;
+      const size_t off = (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 4;
+      st.r[i] = key < a.S ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
+      st.r[4 + i] = key < a.S ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
+    }
+  }
+}
+
+// Transposed store of 4 consecutive rows x 8 columns (bf16) into a
+// [col][row, k-permuted] LDS tile.
+__device__ __forceinline__ void store_transposed4x8(bf16* dst, int row0, int col0, const u32x4* r) {
+  const int pos = kperm_pos(row0);
+#pragma unroll
+  for (int dd = 0; dd < 8; ++dd) {
+    const int w = dd >> 1, sh = (dd & 1) * 16;
+    const uint32_t lo = ((r[0][w] >> sh) & 0xffffu) | (((r[1][w] >> sh) & 0xffffu) << 16);
+    const uint32_t hi = ((r[2][w] >> sh) & 0xffffu) | (((r[3][w] >> sh) & 0xffffu) << 16);
+    st_u32x2(dst + (col0 + dd) * kRow + pos, u32x2{lo, hi});
+  }
+}
+
+template <bool F32>
+__device__ __forceinline__ void dq_store(const BwdArgs& a, int b, int kb, const DqStage<F32>& st,
+                                         DqLds<F32>& lds, int buf) {
+  const int tid = threadIdx.x;
+  if (tid < kStep) lds.kid[buf][tid] = a.kid[(size_t)b * a.tk_pad + kb + tid];
+  if constexpr (!F32) {
+    const int u = tid & 127;
+    const int kg = u >> 3, ch = u & 7;
+    bf16* nat = tid < 128 ? lds.k[buf] : lds.v[buf];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st_u32x4(nat + (kg * 4 + i) * kRow + ch * 8, st.r[i]);
+    if (tid < 128) store_transposed4x8(lds.kt[buf], kg * 4, ch * 8, st.r);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + 256 * i;
+      const int key = u >> 4, ch = u & 15;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lds.k[buf][key * kRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
+        lds.v[buf][key * kRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
+      }
+    }
+  }
+}
+
+template <int HPW, bool F32>
+__global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
+  __shared__ DqLds<F32> lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int hr = blockIdx.x;
+  const int b = hr / (a.Hkv * a.hchunks);
+  const int kvh = (hr / a.hchunks) % a.Hkv;
+  const int hc = hr % a.hchunks;
+  const int qt = blockIdx.y;
+  const int qpos = qt * kTile + wave * 32 + (lane & 31);
+  const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
+  const bool qvalid = qpos < a.T;
+  const bool qactive = qvalid && myqid != 0;
+  int head[HPW];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) head[j] = kvh * a.G + hc * HPW + j;
+
+  constexpr int kQRegs = F32 ? 32 : 4;
+  using QT = typename std::conditional<F32, float, bf16x8>::type;
+  QT qf[HPW][kQRegs], gf[HPW][kQRegs];
+  float lse2[HPW], dlt[HPW];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    const size_t row = (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD;
+    if constexpr (!F32) {
+      const bf16* qs = reinterpret_cast<const bf16*>(a.q) + row + 8 * half;
+      const bf16* gs = reinterpret_cast<const bf16*>(a.dout) + row + 8 * half;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (qvalid) {
+          qf[j][ks] = ld_bf16x8(qs + ks * 16);
+          gf[j][ks] = ld_bf16x8(gs + ks * 16);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            qf[j][ks][e] = (bf16)0.f;
+            gf[j][ks][e] = (bf16)0.f;
+          }
+        }
+      }
+    } else {
+      const float* qs = reinterpret_cast<const float*>(a.q) + row + half;
+      const float* gs = reinterpret_cast<const float*>(a.dout) + row + half;
+#pragma unroll
+      for (int st = 0; st < 32; ++st) {
+        qf[j][st] = qvalid ? qs[2 * st] : 0.f;
+        gf[j][st] = qvalid ? gs[2 * st] : 0.f;
+      }
+    }
+    const size_t li = ((size_t)b * a.Hq + head[j]) * a.T + qpos;
+    lse2[j] = qactive ? a.lse[li] * kLog2e : kPosInf;
+    dlt[j] = qvalid ? a.delta[li] : 0.f;
+  }
+
+  f32x16 dqacc[HPW][2];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    dqacc[j][0] = zero16();
+    dqacc[j][1] = zero16();
+  }
+
+  const int count = a.qcnt[(size_t)b * a.nq + qt];
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
+  const int nsteps = count * (kTile / kStep);
+  const float c = a.scale_log2;
+
+  DqStage<F32> stage;
+  if (nsteps > 0) {
+    const int kb0 = (list[0] >> 2) * kTile;
+    dq_load<F32>(a, b, kvh, kb0, stage);
+    dq_store<F32>(a, b, kb0, stage, lds, 0);
+  }
+  __syncthreads();
+
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1;
+    const int entry = list[step >> 1];
+    const int kb = (entry >> 2) * kTile + (step & 1) * kStep;
+    const bool partial = (entry & 3) == 1;
+    int next_kb = 0;
+    if (step + 1 < nsteps) {
+      const int e2 = list[(step + 1) >> 1];
+      next_kb = (e2 >> 2) * kTile + ((step + 1) & 1) * kStep;
+      dq_load<F32>(a, b, kvh, next_kb, stage);
+    }
+
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      f32x16 s[HPW], dp[HPW];
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) {
+        s[j] = zero16();
+        dp[j] = zero16();
+      }
+      if constexpr (!F32) {
+        const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kRow + 8 * half];
+        const bf16* vrow = &lds.v[buf][(kb2 * 32 + (lane & 31)) * kRow + 8 * half];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 kf = ld_bf16x8(krow + ks * 16);
+          const bf16x8 vf = ld_bf16x8(vrow + ks * 16);
+#pragma unroll
+          for (int j = 0; j < HPW; ++j) {
+            s[j] = mfma32x32x16(kf, qf[j][ks], s[j]);
+            dp[j] = mfma32x32x16(vf, gf[j][ks], dp[j]);
+          }
+        }
+      } else {
+        const float* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kRowF + half];
+        const float* vrow = &lds.v[buf][(kb2 * 32 + (lane & 31)) * kRowF + half];
+#pragma unroll
+        for (int st = 0; st < 32; ++st) {
+          const float kf = krow[2 * st];
+          const float vf = vrow[2 * st];
+#pragma unroll
+          for (int j = 0; j < HPW; ++j) {
+            s[j] = mfma32x32x2(kf, qf[j][st], s[j]);
+            dp[j] = mfma32x32x2(vf, gf[j][st], dp[j]);
+          }
+        }
+      }
+      // P^T and dS^T in place of s
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        bool ok[4] = {true, true, true, true};
+        if (partial) {
+          const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
+          const int4 kids = *reinterpret_cast<const int4*>(&lds.kid[buf][kk0]);
+          const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ok[i] = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = g4 * 4 + i;
+#pragma unroll
+          for (int j = 0; j < HPW; ++j) {
+            const float p = ok[i] ? fast_exp2(fmaf(s[j][r], c, -lse2[j])) : 0.f;
+            s[j][r] = p * (dp[j][r] - dlt[j]);
+          }
+        }
+      }
+      // dQ^T += K^T dS^T
+      if constexpr (!F32) {
+        bf16x8 dsf[HPW][2];
+#pragma unroll
+        for (int j = 0; j < HPW; ++j) {
+          dsf[j][0] = pack8(s[j], 0);
+          dsf[j][1] = pack8(s[j], 8);
+        }
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const bf16* ktrow = &lds.kt[buf][(db * 32 + (lane & 31)) * kRow + kb2 * 32 + 8 * half];
+#pragma unroll
+          for (int ks2 = 0; ks2 < 2; ++ks2) {
+            const bf16x8 af = ld_bf16x8(ktrow + ks2 * 16);
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) dqacc[j][db] = mfma32x32x16(af, dsf[j][ks2], dqacc[j][db]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float af = lds.k[buf][(kb2 * 32 + acc_row(r, lane)) * kRowF + db * 32 + (lane & 31)];
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) dqacc[j][db] = mfma32x32x2(af, s[j][r], dqacc[j][db]);
+          }
+      }
+    }
+
+    if (step + 1 < nsteps) dq_store<F32>(a, b, next_kb, stage, lds, buf ^ 1);
+    __syncthreads();
+  }
+
+  if (!qvalid) return;
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = db * 32 + 8 * g4 + 4 * half;
+        const size_t off = (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + d0;
+        if constexpr (!F32) {
+          bf16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = (bf16)(qactive ? dqacc[j][db][g4 * 4 + i] * a.scale : 0.f);
+          *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dq) + off) = o;
+        } else {
+          f32x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = qactive ? dqacc[j][db][g4 * 4 + i] * a.scale : 0.f;
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dq) + off) = o;
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. dk, dv (per key tile and KV head)
+// ---------------------------------------------------------------------------
+template <bool F32>
+struct KvLds;
+
+template <>
+struct KvLds<false> {
+  bf16 q[2][kStep * kRow];    // Q    [query][d]
+  bf16 g[2][kStep * kRow];    // dO   [query][d]
+  bf16 qt[2][kD * kRow];      // Q^T  [d][query, k-permuted]
+  bf16 gt[2][kD * kRow];      // dO^T [d][query, k-permuted]
+  float lse2[2][kStep];
+  float dlt[2][kStep];
+  int qid[2][kStep];
+};
+
+template <>
+struct KvLds<true> {
+  float q[2][kStep * kRowF];
+  float g[2][kStep * kRowF];
+  float lse2[2][kStep];
+  float dlt[2][kStep];
+  int qid[2][kStep];
+};
+
+template <bool F32>
+struct KvStage {
+  u32x4 r[F32 ? 8 : 4];
+  float lse2, dlt;
+  int qid;
+};
+
+// Iteration `it` of a key tile's loop -> (query tile entry, head in group,
+// 64-query half).
+__device__ __forceinline__ void kv_iter(const BwdArgs& a, const int* list, int it, int& qb,
+                                        int& head_in_group, int& cls) {
+  const int per_tile = a.G * 2;
+  const int entry = list[it / per_tile];
+  const int rem = it % per_tile;
+  head_in_group = rem >> 1;
+  qb = (entry >> 2) * kTile + (rem & 1) * kStep;
+  cls = entry & 3;
+}
+
+template <bool F32>
+__device__ __forceinline__ void kv_load(const BwdArgs& a, int b, int h, int qb, KvStage<F32>& st) {
+  const int tid = threadIdx.x;
+  if constexpr (!F32) {
+    // thread -> (tensor, 4 consecutive queries, one d chunk)
+    const bf16* src = reinterpret_cast<const bf16*>((tid & 1) ? a.dout : a.q);
+    const int u = tid >> 1;
+    const int qg = u >> 3, ch = u & 7;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qq = qb + qg * 4 + i;
+      st.r[i] = qq < a.T ? ld_u32x4(src + (((size_t)b * a.T + qq) * a.Hq + h) * kD + ch * 8)
+                         : u32x4{0, 0, 0, 0};
+    }
+  } else {
+    const float* qs = reinterpret_cast<const float*>(a.q);
+    const float* gs = reinterpret_cast<const float*>(a.dout);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + 256 * i;
+      const int qq = qb + (u >> 4), ch = u & 15;
+      const size_t off = (((size_t)b * a.T + qq) * a.Hq + h) * kD + ch * 4;
+      st.r[i] = qq < a.T ? ld_u32x4(qs + off) : u32x4{0, 0, 0, 0};
+      st.r[4 + i] = qq < a.T ? ld_u32x4(gs + off) : u32x4{0, 0, 0, 0};
+    }
+  }
+  if (tid < kStep) {
+    const int qq = qb + tid;
+    const int id = a.qid[(size_t)b * a.tq_pad + qq];
+    const bool act = qq < a.T && id != 0;
+    const size_t li = ((size_t)b * a.Hq + h) * a.T + qq;
+    st.qid = id;
+    st.lse2 = act ? a.lse[li] * kLog2e : kPosInf;
+    st.dlt = act ? a.delta[li] : 0.f;
+  }
+}
+
+template <bool F32>
+__device__ __forceinline__ void kv_store(const KvStage<F32>& st, KvLds<F32>& lds, int buf) {
+  const int tid = threadIdx.x;
+  if (tid < kStep) {
+    lds.qid[buf][tid] = st.qid;
+    lds.lse2[buf][tid] = st.lse2;
+    lds.dlt[buf][tid] = st.dlt;
+  }
+  if constexpr (!F32) {
+    const int u = tid >> 1;
+    const int qg = u >> 3, ch = u & 7;
+    bf16* nat = (tid & 1) ? lds.g[buf] : lds.q[buf];
+    bf16* tr = (tid & 1) ? lds.gt[buf] : lds.qt[buf];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st_u32x4(nat + (qg * 4 + i) * kRow + ch * 8, st.r[i]);
+    store_transposed4x8(tr, qg * 4, ch * 8, st.r);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + 256 * i;
+      const int qq = u >> 4, ch = u & 15;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lds.q[buf][qq * kRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
+        lds.g[buf][qq * kRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
+      }
+    }
+  }
+}
+
+template <bool F32>
+__global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
+  __shared__ KvLds<F32> lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int b = blockIdx.x / a.Hkv;
+  const int kvh = blockIdx.x % a.Hkv;
+  const int kt = blockIdx.y;
+  const int kpos = kt * kTile + wave * 32 + (lane & 31);
+  const int mykid = a.kid[(size_t)b * a.tk_pad + kpos];
+  const bool kvalid = kpos < a.S;
+
+  // K, V as B operands of S = Q K^T and dP = dO V^T
+  constexpr int kRegs = F32 ? 32 : 4;
+  using KT = typename std::conditional<F32, float, bf16x8>::type;
+  KT kf[kRegs], vf[kRegs];
+  {
+    const size_t row = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD;
+    if constexpr (!F32) {
+      const bf16* ks = reinterpret_cast<const bf16*>(a.k) + row + 8 * half;
+      const bf16* vs = reinterpret_cast<const bf16*>(a.v) + row + 8 * half;
+#pragma unroll
+      for (int ks2 = 0; ks2 < 4; ++ks2) {
+        if (kvalid) {
+          kf[ks2] = ld_bf16x8(ks + ks2 * 16);
+          vf[ks2] = ld_bf16x8(vs + ks2 * 16);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            kf[ks2][e] = (bf16)0.f;
+            vf[ks2][e] = (bf16)0.f;
+          }
+        }
+      }
+    } else {
+      const float* ks = reinterpret_cast<const float*>(a.k) + row + half;
+      const float* vs = reinterpret_cast<const float*>(a.v) + row + half;
+#pragma unroll
+      for (int st = 0; st < 32; ++st) {
+        kf[st] = kvalid ? ks[2 * st] : 0.f;
+        vf[st] = kvalid ? vs[2 * st] : 0.f;
+      }
+    }
+  }
+
+  f32x16 dkacc[2], dvacc[2];
+  dkacc[0] = dkacc[1] = dvacc[0] = dvacc[1] = zero16();
+
+  const int count = a.kcnt[(size_t)b * a.nk + kt];
+  const int* list = a.klist + ((size_t)b * a.nk + kt) * a.nq;
+  const int niters = count * a.G * 2;
+  const float c = a.scale_log2;
+
+  KvStage<F32> stage;
+  if (niters > 0) {
+    int qb, hg, cls;
+    kv_iter(a, list, 0, qb, hg, cls);
+    kv_load<F32>(a, b, kvh * a.G + hg, qb, stage);
+    kv_store<F32>(stage, lds, 0);
+  }
+  __syncthreads();
+
+  for (int it = 0; it < niters; ++it) {
+    const int buf = it & 1;
+    int qb, hg, cls;
+    kv_iter(a, list, it, qb, hg, cls);
+    const bool partial = cls == 1;
+    if (it + 1 < niters) {
+      int qb2, hg2, cls2;
+      kv_iter(a, list, it + 1, qb2, hg2, cls2);
+      kv_load<F32>(a, b, kvh * a.G + hg2, qb2, stage);
+    }
+
+#pragma unroll
+    for (int qb2 = 0; qb2 < 2; ++qb2) {
+      f32x16 s = zero16(), dp = zero16();
+      if constexpr (!F32) {
+        const bf16* qrow = &lds.q[buf][(qb2 * 32 + (lane & 31)) * kRow + 8 * half];
+        const bf16* grow = &lds.g[buf][(qb2 * 32 + (lane & 31)) * kRow + 8 * half];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          s = mfma32x32x16(ld_bf16x8(qrow + ks * 16), kf[ks], s);
+          dp = mfma32x32x16(ld_bf16x8(grow + ks * 16), vf[ks], dp);
+        }
+      } else {
+        const float* qrow = &lds.q[buf][(qb2 * 32 + (lane & 31)) * kRowF + half];
+        const float* grow = &lds.g[buf][(qb2 * 32 + (lane & 31)) * kRowF + half];
+#pragma unroll
+        for (int st = 0; st < 32; ++st) {
+          s = mfma32x32x2(qrow[2 * st], kf[st], s);
+          dp = mfma32x32x2(grow[2 * st], vf[st], dp);
+        }
+      }
+      // rows of s/dp are queries qq = qb2*32 + acc_row(r, lane); column = my key
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int qq0 = qb2 * 32 + 8 * g4 + 4 * half;
+        const float4 l4 = *reinterpret_cast<const float4*>(&lds.lse2[buf][qq0]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&lds.dlt[buf][qq0]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+        bool ok[4] = {true, true, true, true};
+        if (partial) {
+          const int4 ids = *reinterpret_cast<const int4*>(&lds.qid[buf][qq0]);
+          const int iv[4] = {ids.x, ids.y, ids.z, ids.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ok[i] = iv[i] == mykid && (!a.causal || kpos <= qb + qq0 + i);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = g4 * 4 + i;
+          const float p = ok[i] ? fast_exp2(fmaf(s[r], c, -lv[i])) : 0.f;
+          s[r] = p;
+          dp[r] = p * (dp[r] - dv4[i]);
+        }
+      }
+      if constexpr (!F32) {
+        const bf16x8 pf0 = pack8(s, 0), pf1 = pack8(s, 8);
+        const bf16x8 sf0 = pack8(dp, 0), sf1 = pack8(dp, 8);
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const bf16* gtrow = &lds.gt[buf][(db * 32 + (lane & 31)) * kRow + qb2 * 32 + 8 * half];
+          const bf16* qtrow = &lds.qt[buf][(db * 32 + (lane & 31)) * kRow + qb2 * 32 + 8 * half];
+          dvacc[db] = mfma32x32x16(ld_bf16x8(gtrow), pf0, dvacc[db]);
+          dvacc[db] = mfma32x32x16(ld_bf16x8(gtrow + 16), pf1, dvacc[db]);
+          dkacc[db] = mfma32x32x16(ld_bf16x8(qtrow), sf0, dkacc[db]);
+          dkacc[db] = mfma32x32x16(ld_bf16x8(qtrow + 16), sf1, dkacc[db]);
+        }
+      } else {
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int qq = qb2 * 32 + acc_row(r, lane);
+            dvacc[db] = mfma32x32x2(lds.g[buf][qq * kRowF + db * 32 + (lane & 31)], s[r], dvacc[db]);
+            dkacc[db] = mfma32x32x2(lds.q[buf][qq * kRowF + db * 32 + (lane & 31)], dp[r], dkacc[db]);
+          }
+      }
+    }
+
+    if (it + 1 < niters) kv_store<F32>(stage, lds, buf ^ 1);
+    __syncthreads();
+  }
+
+  if (!kvalid) return;
+  const bool kactive = mykid != 0;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = db * 32 + 8 * g4 + 4 * half;
+      const size_t off = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD + d0;
+      if constexpr (!F32) {
+        bf16x4 ok, ov;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ok[i] = (bf16)(kactive ? dkacc[db][g4 * 4 + i] * a.scale : 0.f);
+          ov[i] = (bf16)(kactive ? dvacc[db][g4 * 4 + i] : 0.f);
+        }
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dk) + off) = ok;
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dv) + off) = ov;
+      } else {
+        f32x4 ok, ov;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ok[i] = kactive ? dkacc[db][g4 * 4 + i] * a.scale : 0.f;
+          ov[i] = kactive ? dvacc[db][g4 * 4 + i] : 0.f;
+        }
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dk) + off) = ok;
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dv) + off) = ov;
+      }
+    }
+}
+
+hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
+                           const void* dout, const float* lse, bool f32, int batch, int T, int S,
+                           int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
+                           void* dk, void* dv, float* delta, hipStream_t stream) {
+  BwdArgs a;
+  const PlanLayout lay = plan_layout(batch, T, S);
+  const char* p = reinterpret_cast<const char*>(plan);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.dout = dout;
+  a.lse = lse;
+  a.delta = delta;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.qid = reinterpret_cast<const int*>(p + lay.qid);
+  a.kid = reinterpret_cast<const int*>(p + lay.kid);
+  a.qcnt = reinterpret_cast<const int*>(p + lay.qcnt);
+  a.qlist = reinterpret_cast<const int*>(p + lay.qlist);
+  a.kcnt = reinterpret_cast<const int*>(p + lay.kcnt);
+  a.klist = reinterpret_cast<const int*>(p + lay.klist);
+  a.T = T;
+  a.S = S;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  const int hpw = (a.G % 2 == 0) ? 2 : 1;
+  a.hchunks = a.G / hpw;
+  a.nq = lay.nq;
+  a.nk = lay.nk;
+  a.tq_pad = lay.tq_pad;
+  a.tk_pad = lay.tk_pad;
+  a.causal = mode == 0;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  const size_t rows = (size_t)batch * T * Hq;
+  const unsigned dgrid = (unsigned)((rows + 255) / 256);
+  if (f32)
+    hipLaunchKernelGGL((bwd_delta_kernel<true>), dim3(dgrid), dim3(256), 0, stream, a, batch);
+  else
+    hipLaunchKernelGGL((bwd_delta_kernel<false>), dim3(dgrid), dim3(256), 0, stream, a, batch);
+  const dim3 qgrid(batch * Hkv * a.hchunks, lay.nq);
+  if (f32) {
+    if (hpw == 2)
+      hipLaunchKernelGGL((bwd_dq_kernel<2, true>), qgrid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((bwd_dq_kernel<1, true>), qgrid, dim3(256), 0, stream, a);
+  } else {
+    if (hpw == 2)
+      hipLaunchKernelGGL((bwd_dq_kernel<2, false>), qgrid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((bwd_dq_kernel<1, false>), qgrid, dim3(256), 0, stream, a);
+  }
+  const dim3 kgrid(batch * Hkv, lay.nk);
+  if (f32)
+    hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((bwd_dkdv_kernel<false>), kgrid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mf

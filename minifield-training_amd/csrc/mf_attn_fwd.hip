@@ -1,0 +1,412 @@
+// Flash-style forward for segment-masked GQA attention on gfx950.
+//
+// Work unit: one workgroup = 4 waves = one 128-query tile of one row, for
+// HPW (1 or 2) query heads that share a KV head.  Each wave owns 32 queries
+// for all HPW heads, so every K / V^T fragment it reads from LDS feeds HPW
+// MFMAs (the GQA sharing of K/V tiles).  The workgroup walks the compacted
+// list of non-empty 128-key tiles of its query tile (from the block map) in
+// 64-key steps, double-buffering K and V^T in LDS.
+//
+// Scores are formed transposed, S^T = K Q^T, so an accumulator column is one
+// query: the row max and row sum are in-lane reductions plus one
+// v_permlane32_swap, and the exponentiated block is already in the register
+// layout of the B operand of O^T += V^T P^T.  PARTIAL tiles compare the
+// canonical ids (and causality) per element; FULL tiles skip the compare.
+// Online softmax in base 2 with the logit scale folded into one FMA.
+#include <type_traits>
+
+#include "mf_common.h"
+
+namespace mf {
+
+struct FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  float* lse;
+  const int* qid;
+  const int* kid;
+  const int* qcnt;
+  const int* qlist;
+  int T, S, Hq, Hkv, G, hchunks;
+  int nq, nk, tq_pad, tk_pad;
+  int causal;
+  float scale, scale_log2;
+};
+
+constexpr int kStepK = 64;          // keys per inner step
+constexpr int kLdsRow = kD + 8;     // bf16 row pitch (144 B): conflict-free b128 reads
+constexpr int kLdsRowF = kD + 1;    // fp32 row pitch (65 floats)
+
+template <bool F32>
+struct FwdLds;
+
+template <>
+struct FwdLds<false> {
+  bf16 k[2][kStepK * kLdsRow];   // K    [key][d]
+  bf16 vt[2][kD * kLdsRow];      // V^T  [d][key, k-permuted]
+  int kid[2][kStepK];
+};
+
+template <>
+struct FwdLds<true> {
+  float k[2][kStepK * kLdsRowF];  // K [key][d]
+  float v[2][kStepK * kLdsRowF];  // V [key][d]
+  int kid[2][kStepK];
+};
+
+// Global -> register staging of one 64-key step (K and V) for the workgroup.
+template <bool F32>
+struct FwdStage {
+  u32x4 r[F32 ? 8 : 4];
+};
+
+template <bool F32>
+__device__ __forceinline__ void fwd_load(const FwdArgs& a, int b, int kvh, int kb,
+                                         FwdStage<F32>& st) {
+  const int tid = threadIdx.x;
+  if constexpr (!F32) {
+    const bf16* src = reinterpret_cast<const bf16*>(tid < 128 ? a.v : a.k);
+    if (tid < 128) {
+      // V: 4 consecutive keys x one 8-wide d chunk per thread
+      const int kg = tid >> 3, ch = tid & 7;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb + kg * 4 + i;
+        st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
+                            : u32x4{0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int u = (tid - 128) + 128 * i;
+        const int key = kb + (u >> 3), ch = u & 7;
+        st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
+                            : u32x4{0, 0, 0, 0};
+      }
+    }
+  } else {
+    const float* ks = reinterpret_cast<const float*>(a.k);
+    const float* vs = reinterpret_cast<const float*>(a.v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + 256 * i;
+      const int key = kb + (u >> 4), ch = u & 15;
+      const size_t off = (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 4;
+      st.r[i] = key < a.S ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
+      st.r[4 + i] = key < a.S ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
+    }
+  }
+}
+
+template <bool F32>
+__device__ __forceinline__ void fwd_store(const FwdArgs& a, int b, int kb, const FwdStage<F32>& st,
+                                          FwdLds<F32>& lds, int buf) {
+  const int tid = threadIdx.x;
+  if (tid < kStepK) lds.kid[buf][tid] = a.kid[(size_t)b * a.tk_pad + kb + tid];
+  if constexpr (!F32) {
+    if (tid < 128) {
+      const int kg = tid >> 3, ch = tid & 7;
+      const int pos = kperm_pos(kg * 4);
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) {
+        // element dd of each key's 8-wide chunk: 16-bit lane dd of the u32x4
+        uint32_t lo = 0, hi = 0;
+        const int w = dd >> 1, sh = (dd & 1) * 16;
+        lo = ((st.r[0][w] >> sh) & 0xffffu) | (((st.r[1][w] >> sh) & 0xffffu) << 16);
+        hi = ((st.r[2][w] >> sh) & 0xffffu) | (((st.r[3][w] >> sh) & 0xffffu) << 16);
+        st_u32x2(&lds.vt[buf][(ch * 8 + dd) * kLdsRow + pos], u32x2{lo, hi});
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int u = (tid - 128) + 128 * i;
+        st_u32x4(&lds.k[buf][(u >> 3) * kLdsRow + (u & 7) * 8], st.r[i]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + 256 * i;
+      const int key = u >> 4, ch = u & 15;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lds.k[buf][key * kLdsRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
+        lds.v[buf][key * kLdsRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
+      }
+    }
+  }
+}
+
+template <int HPW, bool F32>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
+  __shared__ FwdLds<F32> lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int hr = blockIdx.x;  // (b, kvh, head chunk)
+  const int b = hr / (a.Hkv * a.hchunks);
+  const int kvh = (hr / a.hchunks) % a.Hkv;
+  const int hc = hr % a.hchunks;
+  const int qt = blockIdx.y;
+  const int qpos = qt * kTile + wave * 32 + (lane & 31);
+  const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
+  const bool qvalid = qpos < a.T;
+  int head[HPW];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) head[j] = kvh * a.G + hc * HPW + j;
+
+  // ---- query fragments (B operand of S^T = K Q^T) -----------------------
+  constexpr int kQRegs = F32 ? 32 : 4;
+  using QT = typename std::conditional<F32, float, bf16x8>::type;
+  QT qf[HPW][kQRegs];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    if constexpr (!F32) {
+      const bf16* src = reinterpret_cast<const bf16*>(a.q) +
+                        (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + 8 * half;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        if (qvalid) {
+          qf[j][ks] = ld_bf16x8(src + ks * 16);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qf[j][ks][e] = (bf16)0.f;
+        }
+      }
+    } else {
+      const float* src = reinterpret_cast<const float*>(a.q) +
+                         (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + half;
+#pragma unroll
+      for (int st = 0; st < 32; ++st) qf[j][st] = qvalid ? src[2 * st] : 0.f;
+    }
+  }
+
+  f32x16 oacc[HPW][2];
+  float m[HPW], l[HPW];
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    oacc[j][0] = zero16();
+    oacc[j][1] = zero16();
+    m[j] = kNegInf;
+    l[j] = 0.f;
+  }
+
+  const int count = a.qcnt[(size_t)b * a.nq + qt];
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
+  const int nsteps = count * (kTile / kStepK);
+  const float c = a.scale_log2;
+
+  FwdStage<F32> stage;
+  if (nsteps > 0) {
+    const int e0 = list[0];
+    fwd_load<F32>(a, b, kvh, (e0 >> 2) * kTile, stage);
+    fwd_store<F32>(a, b, (e0 >> 2) * kTile, stage, lds, 0);
+  }
+  __syncthreads();
+
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1;
+    const int entry = list[step >> 1];
+    const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
+    const bool partial = (entry & 3) == 1;
+    int next_kb = 0;
+    if (step + 1 < nsteps) {
+      const int e2 = list[(step + 1) >> 1];
+      next_kb = (e2 >> 2) * kTile + ((step + 1) & 1) * kStepK;
+      fwd_load<F32>(a, b, kvh, next_kb, stage);
+    }
+
+    // ---- S^T = K Q^T for two 32-key blocks --------------------------------
+    f32x16 s[HPW][2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+      for (int j = 0; j < HPW; ++j) s[j][kb2] = zero16();
+      if constexpr (!F32) {
+        const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kLdsRow + 8 * half];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 af = ld_bf16x8(krow + ks * 16);
+#pragma unroll
+          for (int j = 0; j < HPW; ++j) s[j][kb2] = mfma32x32x16(af, qf[j][ks], s[j][kb2]);
+        }
+      } else {
+        const float* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kLdsRowF + half];
+#pragma unroll
+        for (int st = 0; st < 32; ++st) {
+          const float af = krow[2 * st];
+#pragma unroll
+          for (int j = 0; j < HPW; ++j) s[j][kb2] = mfma32x32x2(af, qf[j][st], s[j][kb2]);
+        }
+      }
+    }
+
+    // ---- element mask on PARTIAL tiles ------------------------------------
+    if (partial) {
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
+          const int4 kids = *reinterpret_cast<const int4*>(&lds.kid[buf][kk0]);
+          const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool ok = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
+#pragma unroll
+            for (int j = 0; j < HPW; ++j)
+              s[j][kb2][g4 * 4 + i] = ok ? s[j][kb2][g4 * 4 + i] : kNegInf;
+          }
+        }
+      }
+    }
+
+    // ---- online softmax (base 2) -------------------------------------------
+#pragma unroll
+    for (int j = 0; j < HPW; ++j) {
+      float mx = kNegInf;
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[j][kb2][r], s[j][kb2][r + 1]));
+      mx = halves_max(mx);
+      const float mnew = fmaxf(m[j], mx);
+      const float msafe = mnew == kNegInf ? 0.f : mnew;
+      const float alpha = fast_exp2((m[j] - msafe) * c);
+      m[j] = mnew;
+      l[j] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        oacc[j][0][r] *= alpha;
+        oacc[j][1][r] *= alpha;
+      }
+      const float mc = msafe * c;
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = fast_exp2(fmaf(s[j][kb2][r], c, -mc));
+          s[j][kb2][r] = p;
+          l[j] += p;
+        }
+    }
+
+    // ---- O^T += V^T P^T -------------------------------------------------------
+    if constexpr (!F32) {
+      bf16x8 pf[HPW][2][2];
+#pragma unroll
+      for (int j = 0; j < HPW; ++j)
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) {
+          pf[j][kb2][0] = pack8(s[j][kb2], 0);
+          pf[j][kb2][1] = pack8(s[j][kb2], 8);
+        }
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const bf16* vrow = &lds.vt[buf][(db * 32 + (lane & 31)) * kLdsRow + 8 * half];
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int ks2 = 0; ks2 < 2; ++ks2) {
+            const bf16x8 vf = ld_bf16x8(vrow + kb2 * 32 + ks2 * 16);
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) oacc[j][db] = mfma32x32x16(vf, pf[j][kb2][ks2], oacc[j][db]);
+          }
+      }
+    } else {
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float vf = lds.v[buf][(kb2 * 32 + acc_row(r, lane)) * kLdsRowF + db * 32 + (lane & 31)];
+#pragma unroll
+            for (int j = 0; j < HPW; ++j) oacc[j][db] = mfma32x32x2(vf, s[j][kb2][r], oacc[j][db]);
+          }
+    }
+
+    if (step + 1 < nsteps) fwd_store<F32>(a, b, next_kb, stage, lds, buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----------------------------------------------------------------
+  const bool qactive = qvalid && myqid != 0;
+#pragma unroll
+  for (int j = 0; j < HPW; ++j) {
+    const float lt = halves_sum(l[j]);
+    const bool has = qactive && lt > 0.f;
+    const float inv = has ? 1.f / lt : 0.f;
+    if (qvalid) {
+      if (half == 0)
+        a.lse[((size_t)b * a.Hq + head[j]) * a.T + qpos] =
+            has ? fmaf(m[j], a.scale, __logf(lt)) : kPosInf;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d0 = db * 32 + 8 * g4 + 4 * half;
+          const size_t off = (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + d0;
+          if constexpr (!F32) {
+            bf16x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = (bf16)(has ? oacc[j][db][g4 * 4 + i] * inv : 0.f);
+            *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.out) + off) = o;
+          } else {
+            f32x4 o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[i] = has ? oacc[j][db][g4 * 4 + i] * inv : 0.f;
+            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + off) = o;
+          }
+        }
+    }
+  }
+}
+
+hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32, int batch,
+                           int T, int S, int Hq, int Hkv, int mode, float scale,
+                           const void* plan, void* out, float* lse, hipStream_t stream) {
+  FwdArgs a;
+  const PlanLayout lay = plan_layout(batch, T, S);
+  const char* p = reinterpret_cast<const char*>(plan);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.lse = lse;
+  a.qid = reinterpret_cast<const int*>(p + lay.qid);
+  a.kid = reinterpret_cast<const int*>(p + lay.kid);
+  a.qcnt = reinterpret_cast<const int*>(p + lay.qcnt);
+  a.qlist = reinterpret_cast<const int*>(p + lay.qlist);
+  a.T = T;
+  a.S = S;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  const int hpw = (a.G % 2 == 0) ? 2 : 1;
+  a.hchunks = a.G / hpw;
+  a.nq = lay.nq;
+  a.nk = lay.nk;
+  a.tq_pad = lay.tq_pad;
+  a.tk_pad = lay.tk_pad;
+  a.causal = mode == 0;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  const dim3 grid(batch * Hkv * a.hchunks, lay.nq);
+  if (f32) {
+    if (hpw == 2)
+      hipLaunchKernelGGL((attn_fwd_kernel<2, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<1, true>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (hpw == 2)
+      hipLaunchKernelGGL((attn_fwd_kernel<2, false>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<1, false>), grid, dim3(256), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mf

@@ -1,0 +1,203 @@
+// Block-mask builder: segment ids + masks -> canonical token ids, per-tile
+// run lists, the EMPTY/PARTIAL/FULL tile map and compacted work lists.
+//
+// Semantics (reference: src/minifield_training/kernels/attention.py:94-107
+// and kernels/bidirectional.py:21-31):
+//   packed causal : active = mask > 0 && seg != 0; pair valid iff both active,
+//                   same segment and key <= query.
+//   packed bidir  : active = mask != 0 && seg != 0; pair valid iff both active
+//                   and same segment.
+//   key-mask bidir: every query of a row with at least one active key is a
+//                   query of "segment" 1; key j is in segment 1 iff mask != 0.
+// Canonical ids: the segment id of an active token, 0 for inactive tokens and
+// for the tile padding past the sequence end.  Useful pairs are pairs of
+// equal NONZERO ids (plus causality), which is exactly the reference grid
+// with the self-fallback rows of inactive queries removed (their outputs are
+// multiplied by 0 in the reference, attention.py:261).
+//
+// Tiles are classified from run-length encodings of the ids, so the cost is
+// O(runs_q * runs_k) per tile pair instead of 128 * 128; it stays exact for
+// arbitrary (non-contiguous, repeated) ids because every run is compared.
+#include "mf_common.h"
+
+namespace mf {
+
+struct MapArgs {
+  const int32_t* seg;
+  const void* mask;
+  int mask_u8;
+  int mode;
+  int batch, q_len, kv_len;
+  PlanLayout lay;
+  char* plan;
+};
+
+__device__ __forceinline__ int* plan_i32(char* plan, size_t off) {
+  return reinterpret_cast<int*>(plan + off);
+}
+
+// One block per (position chunk, row).
+__global__ __launch_bounds__(256) void token_ids_kernel(MapArgs a) {
+  const int b = blockIdx.y;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  int* qid = plan_i32(a.plan, a.lay.qid) + (size_t)b * a.lay.tq_pad;
+  int* kid = plan_i32(a.plan, a.lay.kid) + (size_t)b * a.lay.tk_pad;
+  if (a.mode == 2) {
+    // present = any(mask[b, :]) over the key axis (bidirectional.py:23).
+    int any = 0;
+    for (int j = threadIdx.x; j < a.kv_len; j += blockDim.x)
+      any |= mask_at(a.mask, a.mask_u8, (long)b * a.kv_len + j) != 0;
+    any = __syncthreads_or(any);
+    if (p < a.lay.tq_pad) qid[p] = (p < a.q_len && any) ? 1 : 0;
+    if (p < a.lay.tk_pad)
+      kid[p] = (p < a.kv_len && mask_at(a.mask, a.mask_u8, (long)b * a.kv_len + p) != 0) ? 1 : 0;
+    return;
+  }
+  // packed modes: q_len == kv_len, one id per token
+  const int pad = a.lay.tq_pad > a.lay.tk_pad ? a.lay.tq_pad : a.lay.tk_pad;
+  if (p >= pad) return;
+  int id = 0;
+  if (p < a.q_len) {
+    const long idx = (long)b * a.q_len + p;
+    const int m = mask_at(a.mask, a.mask_u8, idx);
+    const int s = a.seg[idx];
+    const bool active = (a.mode == 0 ? m > 0 : m != 0) && s != 0;
+    id = active ? s : 0;
+  }
+  if (p < a.lay.tq_pad) qid[p] = id;
+  if (p < a.lay.tk_pad) kid[p] = id;
+}
+
+// One wave per (tile, row): tiles [0, nq) are query tiles, [nq, nq+nk) key
+// tiles.  Writes the ordered maximal runs of equal nonzero ids.
+__global__ __launch_bounds__(64) void tile_runs_kernel(MapArgs a) {
+  const int b = blockIdx.y;
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x;
+  const bool is_q = t < a.lay.nq;
+  const int tile = is_q ? t : t - a.lay.nq;
+  const int* ids = is_q ? plan_i32(a.plan, a.lay.qid) + (size_t)b * a.lay.tq_pad
+                        : plan_i32(a.plan, a.lay.kid) + (size_t)b * a.lay.tk_pad;
+  const size_t rec_bytes = sizeof(int) + sizeof(Run) * kMaxRuns;
+  char* rec = a.plan + a.lay.runs +
+              rec_bytes * ((size_t)b * (a.lay.nq + a.lay.nk) + (size_t)t);
+  Run* runs = reinterpret_cast<Run*>(rec + sizeof(int));
+  const int p0 = tile * kTile;
+  int n_start = 0, n_stop = 0;
+  for (int half = 0; half < 2; ++half) {
+    const int i = half * 64 + lane;
+    const int x = ids[p0 + i];
+    const int prev = i > 0 ? ids[p0 + i - 1] : 0;
+    const int next = i < kTile - 1 ? ids[p0 + i + 1] : 0;
+    const bool st = x != 0 && (i == 0 || prev != x);
+    const bool sp = x != 0 && (i == kTile - 1 || next != x);
+    const uint64_t bs = __ballot(st);
+    const uint64_t bp = __ballot(sp);
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    if (st) {
+      const int k = n_start + __popcll(bs & below);
+      runs[k].id = x;
+      runs[k].start = p0 + i;
+    }
+    if (sp) {
+      const int k = n_stop + __popcll(bp & below);
+      runs[k].stop = p0 + i + 1;
+    }
+    n_start += __popcll(bs);
+    n_stop += __popcll(bp);
+  }
+  if (lane == 0) *reinterpret_cast<int*>(rec) = n_start;
+}
+
+// One thread per (q tile, k tile) pair of a row.
+__global__ __launch_bounds__(256) void classify_kernel(MapArgs a) {
+  const int b = blockIdx.y;
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const int nq = a.lay.nq, nk = a.lay.nk;
+  if (idx >= nq * nk) return;
+  const int qi = idx / nk, kj = idx % nk;
+  const bool causal = a.mode == 0;
+  uint8_t cls = 0;
+  if (!(causal && kj > qi)) {
+    const size_t rec_bytes = sizeof(int) + sizeof(Run) * kMaxRuns;
+    const char* base = a.plan + a.lay.runs + rec_bytes * ((size_t)b * (nq + nk));
+    const char* rq_rec = base + rec_bytes * qi;
+    const char* rk_rec = base + rec_bytes * (nq + kj);
+    const int nrq = *reinterpret_cast<const int*>(rq_rec);
+    const int nrk = *reinterpret_cast<const int*>(rk_rec);
+    const Run* rq = reinterpret_cast<const Run*>(rq_rec + sizeof(int));
+    const Run* rk = reinterpret_cast<const Run*>(rk_rec + sizeof(int));
+    bool any = false;
+    for (int x = 0; x < nrq && !any; ++x) {
+      const Run u = rq[x];
+      for (int y = 0; y < nrk; ++y) {
+        const Run w = rk[y];
+        if (u.id == w.id && (!causal || w.start <= u.stop - 1)) {
+          any = true;
+          break;
+        }
+      }
+    }
+    if (any) {
+      cls = 1;
+      if (nrq == 1 && nrk == 1 && rq[0].id == rk[0].id &&
+          rq[0].start == qi * kTile && rq[0].stop == (qi + 1) * kTile &&
+          rk[0].start == kj * kTile && rk[0].stop == (kj + 1) * kTile &&
+          (!causal || kj < qi))
+        cls = 2;
+    }
+  }
+  reinterpret_cast<uint8_t*>(a.plan + a.lay.tmap)[((size_t)b * nq + qi) * nk + kj] = cls;
+}
+
+// One wave per query-tile row (work list of k tiles) or key-tile column
+// (work list of q tiles), compacted in increasing tile order.
+__global__ __launch_bounds__(64) void worklist_kernel(MapArgs a) {
+  const int b = blockIdx.y;
+  const int t = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int nq = a.lay.nq, nk = a.lay.nk;
+  const uint8_t* tmap = reinterpret_cast<const uint8_t*>(a.plan + a.lay.tmap) + (size_t)b * nq * nk;
+  const bool row = t < nq;
+  const int fixed = row ? t : t - nq;
+  const int len = row ? nk : nq;
+  int* list = row ? plan_i32(a.plan, a.lay.qlist) + ((size_t)b * nq + fixed) * nk
+                  : plan_i32(a.plan, a.lay.klist) + ((size_t)b * nk + fixed) * nq;
+  int* count = row ? plan_i32(a.plan, a.lay.qcnt) + (size_t)b * nq + fixed
+                   : plan_i32(a.plan, a.lay.kcnt) + (size_t)b * nk + fixed;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int n = 0;
+  for (int base = 0; base < len; base += 64) {
+    const int i = base + lane;
+    int cls = 0;
+    if (i < len) cls = row ? tmap[(size_t)fixed * nk + i] : tmap[(size_t)i * nk + fixed];
+    const uint64_t bits = __ballot(cls != 0);
+    if (cls != 0) list[n + __popcll(bits & below)] = i * 4 + cls;
+    n += __popcll(bits);
+  }
+  if (lane == 0) *count = n;
+}
+
+hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, int mode,
+                            int batch, int q_len, int kv_len, void* plan,
+                            hipStream_t stream) {
+  MapArgs a;
+  a.seg = seg;
+  a.mask = mask;
+  a.mask_u8 = mask_u8;
+  a.mode = mode;
+  a.batch = batch;
+  a.q_len = q_len;
+  a.kv_len = kv_len;
+  a.lay = plan_layout(batch, q_len, kv_len);
+  a.plan = reinterpret_cast<char*>(plan);
+  const int pad = a.lay.tq_pad > a.lay.tk_pad ? a.lay.tq_pad : a.lay.tk_pad;
+  hipLaunchKernelGGL(token_ids_kernel, dim3((pad + 255) / 256, batch), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(tile_runs_kernel, dim3(a.lay.nq + a.lay.nk, batch), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL(classify_kernel, dim3((a.lay.nq * a.lay.nk + 255) / 256, batch), dim3(256),
+                     0, stream, a);
+  hipLaunchKernelGGL(worklist_kernel, dim3(a.lay.nq + a.lay.nk, batch), dim3(64), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mf

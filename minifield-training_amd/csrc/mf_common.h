@@ -1,0 +1,150 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// MFMA conventions used throughout (CDNA3/CDNA4 32x32 family, wave64):
+//   C[32x32] fp32 accumulator: lane l, register r holds
+//       column n = l % 32, row m = 8*(r/4) + 4*(l/32) + (r%4).
+//   v_mfma_f32_32x32x16_bf16: lane l supplies A[m = l%32][k = 8*(l/32) .. +7]
+//       and B[k = 8*(l/32) .. +7][n = l%32] (8 bf16 each).
+//   v_mfma_f32_32x32x2_f32:   lane l supplies A[m = l%32][k = l/32] and
+//       B[k = l/32][n = l%32] (one float each).
+// A contraction may visit its k indices in any order as long as A and B
+// agree; the kernels use that freedom to feed accumulator registers straight
+// back in as B operands (see acc_row / kperm_pos below).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mf {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kTile = 128;  // block-map tile edge (queries and keys)
+constexpr int kD = 64;      // head dimension served by the kernels
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kPosInf = __builtin_huge_valf();
+
+// Row (within a 32-row accumulator block) held by register r of lane l.
+__device__ __forceinline__ int acc_row(int r, int lane) {
+  return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+
+// Position of key (or query) index kk (0..63 within a 64-block) in the
+// "k-permuted" LDS layout used for transposed operands.  Inside every group
+// of 16, the 4-element runs are stored in the order 0,2,1,3 so that the 8
+// values lane half h needs for one MFMA k-step -- accumulator rows
+// {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1) -- are 8 contiguous slots.
+__device__ __forceinline__ int kperm_pos(int kk) {
+  const int g = (kk >> 2) & 3;                 // 4-run inside the 16-group
+  const int slot = (g == 1) ? 2 : (g == 2) ? 1 : g;
+  return (kk & ~15) | (slot << 2) | (kk & 3);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b,
+                                               const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x2(float a, float b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// v_permlane32_swap with both operands = x leaves, in every lane l, the pair
+// {x[l], x[l ^ 32]} across its two results (which one lands where does not
+// matter for a symmetric combine).
+__device__ __forceinline__ float halves_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float halves_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x),
+                                            false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// 8 consecutive floats -> bf16x8 (round to nearest even).
+__device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
+  bf16x8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = (bf16)v[base + i];
+  return o;
+}
+
+__device__ __forceinline__ bf16x8 ld_bf16x8(const void* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+__device__ __forceinline__ u32x4 ld_u32x4(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ void st_u32x4(void* p, const u32x4& v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+__device__ __forceinline__ void st_u32x2(void* p, const u32x2& v) {
+  *reinterpret_cast<u32x2*>(p) = v;
+}
+
+// Mask element: nonzero means active.
+__device__ __forceinline__ int mask_at(const void* mask, int mask_u8, long idx) {
+  return mask_u8 ? (int)reinterpret_cast<const uint8_t*>(mask)[idx]
+                 : reinterpret_cast<const int32_t*>(mask)[idx];
+}
+
+// Plan section offsets (bytes), shared by host and device code.
+struct PlanLayout {
+  size_t qid, kid, tmap, qcnt, qlist, kcnt, klist, runs, total;
+  int nq, nk, tq_pad, tk_pad;
+};
+
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Per-tile run record written by the block-map builder.
+struct Run {
+  int id, start, stop;  // absolute token positions [start, stop)
+};
+constexpr int kMaxRuns = kTile;  // a 128-token tile has at most 128 runs
+
+__host__ __device__ inline PlanLayout plan_layout(int batch, int q_len, int kv_len) {
+  PlanLayout p;
+  p.nq = (q_len + kTile - 1) / kTile;
+  p.nk = (kv_len + kTile - 1) / kTile;
+  p.tq_pad = p.nq * kTile;
+  p.tk_pad = p.nk * kTile;
+  size_t off = 0;
+  p.qid = off;   off = align256(off + sizeof(int) * (size_t)batch * p.tq_pad);
+  p.kid = off;   off = align256(off + sizeof(int) * (size_t)batch * p.tk_pad);
+  p.tmap = off;  off = align256(off + (size_t)batch * p.nq * p.nk);
+  p.qcnt = off;  off = align256(off + sizeof(int) * (size_t)batch * p.nq);
+  p.qlist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nq * p.nk);
+  p.kcnt = off;  off = align256(off + sizeof(int) * (size_t)batch * p.nk);
+  p.klist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nk * p.nq);
+  // run records: q tiles then k tiles, each (count int + kMaxRuns Runs)
+  p.runs = off;
+  off = align256(off + (sizeof(int) + sizeof(Run) * kMaxRuns) * (size_t)batch * (p.nq + p.nk));
+  p.total = off;
+  return p;
+}
+
+}  // namespace mf

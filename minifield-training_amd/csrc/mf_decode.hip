@@ -1,0 +1,332 @@
+// Ragged KV-cached decode (one query token per row) on gfx950.
+//
+// Split-K over the cache: the valid prefix of every row is cut into chunks
+// of C tokens; a work item is (row, chunk) for one KV head.  A tiny prep
+// kernel turns the per-row lengths into chunk offsets (a prefix sum on the
+// device, so the host never reads the lengths back), then a persistent grid
+// walks the flattened item list.  Each item streams its chunk of K and V for
+// one KV head into LDS with fully coalesced 16-byte loads (8 lanes cover one
+// 128-byte key row), scores the G query heads of the group against it, and
+// writes a partial (max, sum, unnormalised output).  A combine kernel merges
+// a row's partials with the usual log-sum-exp rescaling.
+//
+// Reference semantics: kernels/attention.py:264-282 -- slot j of row b is
+// valid iff j < valid_length[b]; a length above the capacity reads every
+// slot; a length <= 0 leaves every slot masked, which the reference turns
+// into a uniform average over all slots (the softmax of a constant row).
+#include <type_traits>
+
+#include "mf_common.h"
+
+namespace mf {
+
+struct DecArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* lengths;
+  void* out;
+  int* offsets;    // [B + 1] chunk offsets
+  float* partial;  // [B][Hq][maxc][2 + D]: (scaled max, sum, acc[D])
+  int B, cap, Hq, Hkv, G, maxc, chunk;
+  float scale_log2;
+};
+
+constexpr int kPitch = kD + 8;    // bf16 LDS row pitch (144 B)
+constexpr int kPitchF = kD + 4;   // fp32 LDS row pitch (272 B)
+constexpr int kMaxG = 8;          // query heads per KV head served by decode
+
+__device__ __forceinline__ int eff_len(int len, int cap) {
+  return len <= 0 ? cap : (len > cap ? cap : len);
+}
+
+__global__ __launch_bounds__(256) void decode_prep_kernel(DecArgs a) {
+  // Block-wide exclusive scan of per-row chunk counts (B may exceed 256).
+  __shared__ int part[256];
+  __shared__ int carry;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base < a.B; base += 256) {
+    const int b = base + threadIdx.x;
+    const int n = b < a.B ? (eff_len(a.lengths[b], a.cap) + a.chunk - 1) / a.chunk : 0;
+    part[threadIdx.x] = n;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+      const int x = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+      __syncthreads();
+      part[threadIdx.x] += x;
+      __syncthreads();
+    }
+    if (b < a.B) a.offsets[b] = carry + part[threadIdx.x] - n;
+    __syncthreads();
+    if (threadIdx.x == 255) carry += part[255];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) a.offsets[a.B] = carry;
+}
+
+template <bool F32>
+struct DecLds;
+
+template <>
+struct DecLds<false> {
+  bf16 k[256 * kPitch];
+  bf16 v[256 * kPitch];
+  float p[kMaxG][256];
+  float q[kMaxG][kD];
+  float red[kMaxG][4];
+  float acc[4][kMaxG][kD];
+};
+
+template <>
+struct DecLds<true> {
+  float k[128 * kPitchF];
+  float v[128 * kPitchF];
+  float p[kMaxG][256];
+  float q[kMaxG][kD];
+  float red[kMaxG][4];
+  float acc[4][kMaxG][kD];
+};
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+template <bool F32>
+__global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
+  __shared__ DecLds<F32> lds;
+  constexpr int C = F32 ? 128 : 256;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int kvh = blockIdx.y;
+  const int total = a.offsets[a.B];
+  const float c = a.scale_log2;
+
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    // row of this item: last b with offsets[b] <= item
+    int lo = 0, hi = a.B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (a.offsets[mid] <= item) lo = mid; else hi = mid - 1;
+    }
+    const int b = lo;
+    const int chunk = item - a.offsets[b];
+    const int raw = a.lengths[b];
+    const bool uniform = raw <= 0;
+    const int len = eff_len(raw, a.cap);
+    const int t0 = chunk * C;
+    const int n = min(C, len - t0);
+
+    // ---- stage K, V chunk and the group's queries -------------------------
+    if constexpr (!F32) {
+      const bf16* ks = reinterpret_cast<const bf16*>(a.k);
+      const bf16* vs = reinterpret_cast<const bf16*>(a.v);
+      u32x4 kr[8], vr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int u = tid + 256 * i;
+        const int t = u >> 3, ch = u & 7;
+        const size_t off = (((size_t)b * a.cap + t0 + t) * a.Hkv + kvh) * kD + ch * 8;
+        kr[i] = t < n ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
+        vr[i] = t < n ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int u = tid + 256 * i;
+        st_u32x4(&lds.k[(u >> 3) * kPitch + (u & 7) * 8], kr[i]);
+        st_u32x4(&lds.v[(u >> 3) * kPitch + (u & 7) * 8], vr[i]);
+      }
+      for (int e = tid; e < a.G * kD; e += 256) {
+        const int g = e / kD, d = e % kD;
+        lds.q[g][d] = (float)reinterpret_cast<const bf16*>(a.q)[((size_t)b * a.Hq + kvh * a.G + g) * kD + d];
+      }
+    } else {
+      const float* ks = reinterpret_cast<const float*>(a.k);
+      const float* vs = reinterpret_cast<const float*>(a.v);
+      u32x4 kr[8], vr[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int u = tid + 256 * i;
+        const int t = u >> 4, ch = u & 15;
+        const size_t off = (((size_t)b * a.cap + t0 + t) * a.Hkv + kvh) * kD + ch * 4;
+        kr[i] = t < n ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
+        vr[i] = t < n ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int u = tid + 256 * i;
+        st_u32x4(&lds.k[(u >> 4) * kPitchF + (u & 15) * 4], kr[i]);
+        st_u32x4(&lds.v[(u >> 4) * kPitchF + (u & 15) * 4], vr[i]);
+      }
+      for (int e = tid; e < a.G * kD; e += 256) {
+        const int g = e / kD, d = e % kD;
+        lds.q[g][d] = reinterpret_cast<const float*>(a.q)[((size_t)b * a.Hq + kvh * a.G + g) * kD + d];
+      }
+    }
+    __syncthreads();
+
+    // ---- scores: thread t owns token t ---------------------------------------
+    float sc[kMaxG];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) sc[g] = 0.f;
+    if (tid < n && !uniform) {
+      if constexpr (!F32) {
+#pragma unroll
+        for (int c8 = 0; c8 < 8; ++c8) {
+          const bf16x8 kx = ld_bf16x8(&lds.k[tid * kPitch + c8 * 8]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float kv = (float)kx[e];
+#pragma unroll
+            for (int g = 0; g < kMaxG; ++g)
+              if (g < a.G) sc[g] = fmaf(lds.q[g][c8 * 8 + e], kv, sc[g]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int c4 = 0; c4 < 16; ++c4) {
+          const f32x4 kx = *reinterpret_cast<const f32x4*>(&lds.k[tid * kPitchF + c4 * 4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int g = 0; g < kMaxG; ++g)
+              if (g < a.G) sc[g] = fmaf(lds.q[g][c4 * 4 + e], kx[e], sc[g]);
+        }
+      }
+    }
+    // chunk max and exponentials per head (log2 domain)
+    float mx2[kMaxG];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) {
+      if (g >= a.G) break;
+      const float s2 = tid < n ? sc[g] * c : kNegInf;
+      const float wm = wave_max(s2);
+      if (lane == 0) lds.red[g][wave] = wm;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) {
+      if (g >= a.G) break;
+      mx2[g] = fmaxf(fmaxf(lds.red[g][0], lds.red[g][1]), fmaxf(lds.red[g][2], lds.red[g][3]));
+      const float p = tid < n ? fast_exp2(fmaf(sc[g], c, -mx2[g])) : 0.f;
+      if (tid < C) lds.p[g][tid] = p;
+    }
+    __syncthreads();
+    float lsum[kMaxG];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) {
+      if (g >= a.G) break;
+      const float ws = wave_sum(tid < C ? lds.p[g][tid] : 0.f);
+      lsum[g] = ws;
+    }
+    __syncthreads();  // everyone has read red[] for the max
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) {
+      if (g >= a.G) break;
+      if (lane == 0) lds.red[g][wave] = lsum[g];
+    }
+
+    // ---- PV: thread (d = lane, token group = wave) ---------------------------
+    float acc[kMaxG];
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g) acc[g] = 0.f;
+    for (int t = wave; t < n; t += 4) {
+      float vv;
+      if constexpr (!F32) vv = (float)lds.v[t * kPitch + lane];
+      else vv = lds.v[t * kPitchF + lane];
+#pragma unroll
+      for (int g = 0; g < kMaxG; ++g)
+        if (g < a.G) acc[g] = fmaf(lds.p[g][t], vv, acc[g]);
+    }
+#pragma unroll
+    for (int g = 0; g < kMaxG; ++g)
+      if (g < a.G) lds.acc[wave][g][lane] = acc[g];
+    __syncthreads();
+    if (wave == 0) {
+      for (int g = 0; g < a.G; ++g) {
+        const float o = lds.acc[0][g][lane] + lds.acc[1][g][lane] + lds.acc[2][g][lane] +
+                        lds.acc[3][g][lane];
+        const int h = kvh * a.G + g;
+        float* dst = a.partial + (((size_t)b * a.Hq + h) * a.maxc + chunk) * (2 + kD);
+        dst[2 + lane] = o;
+        if (lane == 0) dst[0] = mx2[g];
+        if (lane == 1) dst[1] = lds.red[g][0] + lds.red[g][1] + lds.red[g][2] + lds.red[g][3];
+      }
+    }
+    __syncthreads();  // LDS reused by the next item
+  }
+}
+
+// One wave per (row, query head): lane = d.
+template <bool F32>
+__global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
+  const int bh = blockIdx.x;
+  const int b = bh / a.Hq;
+  const int lane = threadIdx.x;
+  const int nch = a.offsets[b + 1] - a.offsets[b];
+  const float* src = a.partial + (size_t)bh * a.maxc * (2 + kD);
+  float M = kNegInf;
+  for (int ch = 0; ch < nch; ++ch) M = fmaxf(M, src[ch * (2 + kD)]);
+  float L = 0.f, acc = 0.f;
+  for (int ch = 0; ch < nch; ++ch) {
+    const float w = fast_exp2(src[ch * (2 + kD)] - M);
+    L = fmaf(src[ch * (2 + kD) + 1], w, L);
+    acc = fmaf(src[ch * (2 + kD) + 2 + lane], w, acc);
+  }
+  const float o = acc / L;
+  if constexpr (!F32) reinterpret_cast<bf16*>(a.out)[(size_t)bh * kD + lane] = (bf16)o;
+  else reinterpret_cast<float*>(a.out)[(size_t)bh * kD + lane] = o;
+}
+
+size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk) {
+  const int maxc = (cap + chunk - 1) / chunk;
+  return align256(sizeof(int) * (size_t)(batch + 1)) +
+         sizeof(float) * (size_t)batch * Hq * maxc * (2 + kD);
+}
+
+int decode_chunk(bool f32) { return f32 ? 128 : 256; }
+
+hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
+                         bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
+                         void* workspace, hipStream_t stream) {
+  DecArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.lengths = lengths;
+  a.out = out;
+  a.B = batch;
+  a.cap = cap;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  a.chunk = decode_chunk(f32);
+  a.maxc = (cap + a.chunk - 1) / a.chunk;
+  a.scale_log2 = scale * kLog2e;
+  char* ws = reinterpret_cast<char*>(workspace);
+  a.offsets = reinterpret_cast<int*>(ws);
+  a.partial = reinterpret_cast<float*>(ws + align256(sizeof(int) * (size_t)(batch + 1)));
+  hipLaunchKernelGGL(decode_prep_kernel, dim3(1), dim3(256), 0, stream, a);
+  const int upper = batch * a.maxc;
+  int gx = (1024 + Hkv - 1) / Hkv;
+  if (gx > upper) gx = upper;
+  if (gx < 1) gx = 1;
+  if (f32) {
+    hipLaunchKernelGGL((decode_kernel<true>), dim3(gx, Hkv), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((decode_combine_kernel<true>), dim3(batch * Hq), dim3(64), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((decode_kernel<false>), dim3(gx, Hkv), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((decode_combine_kernel<false>), dim3(batch * Hq), dim3(64), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mf

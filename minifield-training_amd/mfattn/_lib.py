@@ -1,0 +1,123 @@
+"""ctypes binding of ``libmfattn.so`` (the C ABI declared in ``include/mfattn.h``).
+
+The library is loaded at import.  There is no fallback: if it is missing or
+does not load, importing this module raises ``ImportError`` naming the file
+and the build command, so nothing can silently run another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmfattn.so"
+
+# status codes (include/mfattn.h)
+OK = 0
+ERR_INVALID_ARGUMENT = -1
+ERR_SHAPE = -2
+ERR_HEADS = -3
+ERR_HEAD_DIM = -4
+ERR_DTYPE = -5
+ERR_MODE = -6
+ERR_WORKSPACE = -7
+ERR_HIP = -9
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+MASK_I32 = 0
+MASK_U8 = 1
+
+MODE_PACKED_CAUSAL = 0
+MODE_PACKED_BIDIR = 1
+MODE_KEYMASK_BIDIR = 2
+
+TILE = 128
+HEAD_DIM = 64
+
+EXPORTS = (
+    "mf_plan_layout",
+    "mf_plan_bytes",
+    "mf_block_map",
+    "mf_attn_fwd",
+    "mf_attn_bwd_workspace_bytes",
+    "mf_attn_bwd",
+    "mf_decode_workspace_bytes",
+    "mf_decode",
+    "mf_last_error",
+    "mf_version",
+)
+
+
+class MfError(RuntimeError):
+    """A failed C-ABI call; ``code`` is the MF_ERR_* status."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class MfValueError(MfError, ValueError):
+    """Invalid shapes, dtypes or modes (the reference raises ValueError)."""
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"mfattn native library missing: {LIB_PATH} (build it with "
+            "`python -m mfattn.build` from minifield-training_amd/)"
+        )
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+    except OSError as exc:  # pragma: no cover - depends on the machine
+        raise ImportError(f"mfattn native library failed to load: {exc}") from exc
+    vp, i32, sz, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_float
+    lib.mf_plan_layout.argtypes = [i32, i32, i32, ctypes.POINTER(sz)]
+    lib.mf_plan_layout.restype = None
+    lib.mf_plan_bytes.argtypes = [i32, i32, i32]
+    lib.mf_plan_bytes.restype = sz
+    lib.mf_block_map.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]
+    lib.mf_block_map.restype = i32
+    lib.mf_attn_fwd.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, f32, vp, sz,
+                                vp, vp, vp]
+    lib.mf_attn_fwd.restype = i32
+    lib.mf_attn_bwd_workspace_bytes.argtypes = [i32, i32, i32]
+    lib.mf_attn_bwd_workspace_bytes.restype = sz
+    lib.mf_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
+                                f32, vp, sz, vp, vp, vp, vp, sz, vp]
+    lib.mf_attn_bwd.restype = i32
+    lib.mf_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    lib.mf_decode_workspace_bytes.restype = sz
+    lib.mf_decode.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]
+    lib.mf_decode.restype = i32
+    lib.mf_last_error.argtypes = []
+    lib.mf_last_error.restype = ctypes.c_char_p
+    lib.mf_version.argtypes = []
+    lib.mf_version.restype = ctypes.c_char_p
+    return lib
+
+
+LIB = _load()
+
+_VALUE_CODES = {ERR_SHAPE, ERR_HEADS, ERR_HEAD_DIM, ERR_DTYPE, ERR_MODE, ERR_INVALID_ARGUMENT,
+                ERR_WORKSPACE}
+
+
+def check(rc: int) -> None:
+    """Raise for a nonzero status with the library's own message."""
+    if rc == OK:
+        return
+    message = LIB.mf_last_error().decode()
+    if rc in _VALUE_CODES:
+        raise MfValueError(rc, message)
+    raise MfError(rc, message)
+
+
+def plan_layout(batch: int, q_len: int, kv_len: int) -> list[int]:
+    out = (ctypes.c_size_t * 9)()
+    LIB.mf_plan_layout(batch, q_len, kv_len, out)
+    return list(out)
+
+
+def version() -> str:
+    return LIB.mf_version().decode()

@@ -1,0 +1,74 @@
+"""Build ``libmfattn.so`` (the HIP kernels + C ABI) in-tree for gfx950.
+
+``python -m mfattn.build`` (from ``minifield-training_amd/``) or
+``mfattn.build.build()``.  Every ``.hip`` file under ``csrc/`` is compiled
+with ``hipcc --offload-arch=gfx950`` into an object in ``csrc/_build`` and
+linked into ``mfattn/libmfattn.so``.  Packed-FP32 instructions are disabled
+(``-packed-fp32-ops``); the host pass warns that it does not know that
+feature, which is harmless.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import pathlib
+import shutil
+import subprocess
+import sys
+
+PKG = pathlib.Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = ROOT / "csrc"
+OUT = PKG / "libmfattn.so"
+ARCH = "gfx950"
+
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def _hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; the mfattn kernels need ROCm's hipcc")
+    return path
+
+
+def _compile(src: pathlib.Path, obj: pathlib.Path) -> None:
+    cmd = [_hipcc(), *FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(l for l in proc.stderr.splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = True) -> pathlib.Path:
+    sources = sorted(CSRC.glob("*.hip"))
+    objdir = CSRC / "_build"
+    objdir.mkdir(exist_ok=True)
+    objs = [objdir / (s.stem + ".o") for s in sources]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(sources))) as pool:
+        list(pool.map(_compile, sources, objs))
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    os.replace(tmp, OUT)
+    if verbose:
+        print(f"built {OUT}")
+    return OUT
+
+
+if __name__ == "__main__":
+    build()

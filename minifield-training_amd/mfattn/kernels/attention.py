@@ -1,0 +1,135 @@
+"""Packed causal and KV-cached attention with the reference's signatures.
+
+Mirrors ``src/minifield_training/kernels/attention.py`` of the reference:
+
+* ``dense_packed_causal_attention`` -- ``attention.py:245-261``
+* ``packed_causal_attention``       -- ``attention.py:571-588`` (dispatcher)
+* ``dense_cached_attention``        -- ``attention.py:264-282``
+* ``cached_attention``              -- ``attention.py:591-610`` (dispatcher)
+
+Operands are torch tensors on a ROCm device in the reference's BTHD layout;
+every call runs the HIP kernels of ``libmfattn.so`` (block map + flash
+forward, HIP backward through autograd; split-K decode).  The reference's
+backend names (``dense``, ``cudnn``, ``splash``) all name the same
+mathematical function; on MI355X each of them, and ``hip``, runs the HIP
+implementation.  Unknown names raise the reference's ``ValueError``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib, ops
+from ._common import fit_head_dim
+
+
+def dense_packed_causal_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    attention_mask: torch.Tensor,
+    segment_ids: torch.Tensor,
+) -> torch.Tensor:
+    """Causal attention confined to same-segment active tokens.
+
+    A query sees key ``j`` iff ``j <= i``, both share one nonzero segment id
+    and both are mask-active (``attention_mask > 0``); inactive query rows are
+    zero.  Output has the query's shape and dtype.
+    """
+    # the reference's own (weak) shape check, attention.py:92-93
+    if query.shape != key.shape and key.shape != value.shape:
+        raise ValueError("Packed attention query/KV shapes are incompatible")
+    (q, k, v), d = fit_head_dim(query, key, value)
+    out = ops.packed_attention(q, k, v, attention_mask, segment_ids,
+                               _lib.MODE_PACKED_CAUSAL, d ** -0.5)
+    return out[..., :d] if out.shape[-1] != d else out
+
+
+_PACKED_BACKENDS = {
+    "dense": dense_packed_causal_attention,
+    "cudnn": dense_packed_causal_attention,
+    "splash": dense_packed_causal_attention,
+    "hip": dense_packed_causal_attention,
+}
+
+
+def packed_causal_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    attention_mask: torch.Tensor,
+    segment_ids: torch.Tensor,
+    *,
+    backend: str,
+) -> torch.Tensor:
+    """Apply causal attention confined to same-segment active tokens."""
+    try:
+        fn = _PACKED_BACKENDS[backend]
+    except KeyError:
+        raise ValueError(f"Unsupported packed attention backend: {backend}") from None
+    return fn(query, key, value, attention_mask, segment_ids)
+
+
+def _lengths(valid_length, batch: int, device: torch.device) -> torch.Tensor:
+    if isinstance(valid_length, torch.Tensor):
+        lengths = valid_length.to(device=device, dtype=torch.int32).reshape(-1)
+    else:
+        lengths = torch.tensor(valid_length, dtype=torch.int32, device=device).reshape(-1)
+    if lengths.numel() == 1:
+        lengths = lengths.expand(batch)
+    if lengths.numel() != batch:
+        raise ValueError("valid_length must be a scalar or hold one length per row")
+    return lengths.contiguous()
+
+
+def dense_cached_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    valid_length,
+) -> torch.Tensor:
+    """Attend one query per row to the valid prefix of a fixed-size KV cache.
+
+    Non-causal by design: slot ``j`` of row ``b`` is visible iff
+    ``j < valid_length[b]`` (``valid_length`` a scalar or ``[B]``).
+    """
+    if query.shape[-1] != key.shape[-1] or key.shape != value.shape:
+        raise ValueError("Cached attention query/KV shapes are incompatible")
+    if query.shape[2] % key.shape[2]:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if query.shape[1] != 1:
+        # the reference broadcasts the same key set to every query row
+        outs = [dense_cached_attention(query[:, i : i + 1], key, value, valid_length)
+                for i in range(query.shape[1])]
+        return torch.cat(outs, dim=1)
+    (q, k, v), d = fit_head_dim(query.contiguous(), key.contiguous(), value.contiguous())
+    lengths = _lengths(valid_length, query.shape[0], query.device)
+    out = ops.decode(q, k, v, lengths, d ** -0.5)
+    return out[..., :d] if out.shape[-1] != d else out
+
+
+_CACHED_BACKENDS = {
+    "dense": dense_cached_attention,
+    "cudnn": dense_cached_attention,
+    "hip": dense_cached_attention,
+}
+
+
+def cached_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    valid_length,
+    *,
+    backend: str = "cudnn",
+) -> torch.Tensor:
+    """Attend one query to the valid prefix of a fixed-size KV cache.
+
+    Accepts ``dense``, ``cudnn`` and ``hip`` (the reference has no Splash
+    decode, ``attention.py:599-604``).
+    """
+    try:
+        fn = _CACHED_BACKENDS[backend]
+    except KeyError:
+        raise ValueError(f"Unsupported cached attention backend: {backend}") from None
+    return fn(query, key, value, valid_length)

@@ -1,0 +1,42 @@
+"""Test configuration: markers, import paths and the in-tree native build."""
+
+from __future__ import annotations
+
+import pathlib
+import sys
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+PKG_DIR = ROOT / "minifield-training_amd"
+for path in (ROOT, PKG_DIR):
+    if str(path) not in sys.path:
+        sys.path.insert(0, str(path))
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs on the GPU box)")
+
+
+def _ensure_library() -> None:
+    lib = PKG_DIR / "mfattn" / "libmfattn.so"
+    if not lib.exists():
+        # load build.py by path: importing the package would need the library
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("_mfattn_build", PKG_DIR / "mfattn" / "build.py")
+        module = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(module)
+        module.build(verbose=False)
+
+
+_ensure_library()
+
+
+@pytest.fixture(scope="session")
+def device():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    return torch.device("cuda:0")

@@ -1,0 +1,271 @@
+"""GPU parity of the packed attention forward and backward.
+
+Bars: fp32 within 1e-5 (relative, with a 1e-5 floor) of
+the FP64 oracle; bf16 outputs and gradients within max-abs 2e-2 of an fp32
+evaluation of the same bf16 inputs, and within 2e-2 of the reference's bf16
+cast-point emulation where that fits on the CPU.
+"""
+
+import json
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import DT, max_abs, operands, say, torch_reference
+from mfattn import _lib, ops
+from mfattn.kernels import attention, bidirectional
+from oracle import attention as oatt
+from oracle import masks, packing
+
+GOLD = pathlib.Path(__file__).parent / "golden"
+FIX = json.loads((GOLD / "reference_fixtures.json").read_text())
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+
+
+def _grads(fn, q, k, v, do):
+    q, k, v = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
+    out = fn(q, k, v)
+    out.backward(do)
+    return out.detach(), q.grad, k.grad, v.grad
+
+
+def _c1_inputs(device):
+    import sys
+    sys.path.insert(0, str(GOLD))
+    from make_golden import c1_inputs  # noqa: E402
+
+    w, q, k, v, do = c1_inputs()
+    t = lambda x: torch.tensor(x, device=device)  # noqa: E731
+    return w, t(q), t(k), t(v), t(do)
+
+
+def test_c1_fp32_forward_backward_matches_fp64_oracle_and_golden(device):
+    say("C1 fp32 fwd+bwd packed causal")
+    w, q, k, v, do = _c1_inputs(device)
+    mask = torch.tensor(w.attention_mask, device=device)
+    seg = torch.tensor(w.segment_ids, device=device)
+    out, dq, dk, dv = _grads(
+        lambda a, b, c: attention.packed_causal_attention(a, b, c, mask, seg, backend="dense"),
+        q, k, v, do)
+    gold = np.load(GOLD / "c1_fp64.npz")
+    np.testing.assert_allclose(gold["checksums"], [x.double().sum().item() for x in (q, k, v, do)],
+                               rtol=1e-12)
+    ref = oatt.packed_causal_fp64(*(x.cpu().numpy() for x in (q, k, v)), w.attention_mask,
+                                  w.segment_ids)
+    ref_grads = oatt.vjp_fp64(*(x.cpu().numpy() for x in (q, k, v)), ref[1], ref[2], do.cpu().numpy())
+    for got, live, stored in zip((out, dq, dk, dv), (ref[0], *ref_grads),
+                                 (gold["out"], gold["dq"], gold["dk"], gold["dv"])):
+        np.testing.assert_allclose(got.cpu().numpy(), live, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(got.cpu().numpy(), stored, rtol=1e-5, atol=1e-5)
+
+
+def test_reference_packed_fixture_fp32(device):
+    """tests/kernels/test_attention.py:306-345 operands (D=8, seed 2)."""
+    dims = FIX["attention_dims"]
+    say("reference packed fixture D=8")
+    rng = np.random.default_rng(dims["packed_seed"])
+    shapes = [(2, 6, 4, 8), (2, 6, 2, 8), (2, 6, 2, 8)]
+    q, k, v = (rng.normal(size=s).astype(np.float32) for s in shapes)
+    mask = np.array(FIX["layouts"]["attention_packed"]["mask"], np.int32)
+    seg = np.array(FIX["layouts"]["attention_packed"]["segment_ids"], np.int32)
+    t = lambda x: torch.tensor(x, device=device)  # noqa: E731
+    out = attention.dense_packed_causal_attention(t(q), t(k), t(v), t(mask), t(seg))
+    ref = oatt.packed_causal_fp64(q, k, v, mask, seg)[0]
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    assert out.shape == (2, 6, 4, 8)
+
+
+@pytest.mark.parametrize("mask_dtype", [torch.int32, torch.bool])
+def test_bidirectional_uniform_fixture(mask_dtype, device):
+    f = FIX["bidirectional"]["uniform"]
+    say("bidirectional uniform fixture", mask_dtype)
+    q = torch.zeros(f["query_shape"], device=device)
+    k = torch.zeros(f["key_shape"], device=device)
+    values = torch.tensor(f["values"], device=device)
+    mask = torch.tensor(f["mask"], device=device).to(mask_dtype)
+    out = bidirectional.attention(q, k, values, mask)
+    np.testing.assert_allclose(out.cpu().numpy(), np.broadcast_to(f["output_row"], (1, 3, 2, 2)),
+                               rtol=1e-6)
+    vv = values.clone().requires_grad_(True)
+    bidirectional.attention(q, k, vv, mask).sum().backward()
+    np.testing.assert_allclose(vv.grad.cpu().numpy(), f["value_grad_of_sum"], rtol=1e-6)
+    empty = bidirectional.attention(q, k, values, torch.zeros_like(mask))
+    assert (empty == 0).all()
+
+
+def test_bidirectional_packed_fixture(device):
+    f = FIX["bidirectional"]["packed"]
+    say("bidirectional packed fixture")
+    q = torch.zeros(f["query_shape"], device=device)
+    k = torch.zeros(f["key_shape"], device=device)
+    values = torch.tensor(f["values"], device=device).reshape(1, 6, 1, 2)
+    seg = torch.tensor(f["segment_ids"], device=device)
+    out = bidirectional.attention(q, k, values, seg != 0, seg)
+    expected = np.broadcast_to(np.array(f["output_rows"], float)[None, :, None], (1, 6, 2, 2))
+    np.testing.assert_allclose(out.cpu().numpy(), expected, rtol=1e-6)
+    vv = values.clone().requires_grad_(True)
+    bidirectional.attention(q, k, vv, seg != 0, seg).sum().backward()
+    np.testing.assert_allclose(vv.grad.reshape(6, 2).cpu().numpy(), f["value_grad_of_sum"], rtol=1e-6)
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_random_layouts_against_oracle(mode, dtype, device):
+    """Ragged T, non-contiguous ids, masked holes, GQA 2; FP64 oracle."""
+    rng = np.random.default_rng(40 + mode)
+    b, t, hq, hkv = 2, 333, 4, 2
+    s = 200 if mode == 2 else t
+    say("random layout", mode, dtype, (b, t, s))
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, DT[dtype], 0.5, s=s)
+    if mode == 2:
+        mask = (rng.random((b, s)) > 0.3).astype(np.int32)
+        mask[1] = 0
+        seg = None
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, torch.tensor(mask, device=device))  # noqa: E731
+    else:
+        seg = np.repeat(rng.integers(0, 5, size=(b, t // 37 + 1)), 37, axis=1)[:, :t].astype(np.int32)
+        mask = (rng.random((b, t)) > 0.1).astype(np.int32)
+        tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+        if mode == 0:
+            fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+        else:
+            fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = oatt.grouped_fp64(mode, *(x.float().cpu().numpy() for x in (q, k, v)), mask, seg,
+                            d_out=do.float().cpu().numpy())
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        if dtype == "float32":
+            np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
+        else:
+            assert np.abs(a.float().cpu().numpy() - r).max() < BF16_TOL, name
+
+
+@pytest.mark.parametrize("hq, hkv", [(4, 4), (8, 2), (6, 2), (3, 1)])
+def test_gqa_ratios(hq, hkv, device):
+    rng = np.random.default_rng(hq * 10 + hkv)
+    b, t = 1, 256
+    say("gqa", hq, hkv)
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, torch.float32, 0.5)
+    seg = np.repeat([[1, 2, 3, 0]], [100, 90, 50, 16], axis=1).astype(np.int32)
+    ts = torch.tensor(seg, device=device)
+    got = _grads(lambda a, bb, c: bidirectional.attention(a, bb, c, ts != 0, ts), q, k, v, do)
+    ref = oatt.grouped_fp64(1, *(x.cpu().numpy() for x in (q, k, v)), seg != 0, seg,
+                            d_out=do.cpu().numpy())
+    for a, r in zip(got, ref):
+        np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("name", ["C2", "C3", "C5"])
+def test_baseline_config_bf16_fwd_bwd(name, device):
+    """Full BASELINE shapes against the fp32 per-segment torch reference."""
+    w = packing.make_workload(name)
+    mode = masks.MODE_PACKED_CAUSAL if w.causal else masks.MODE_PACKED_BIDIR
+    say("baseline", name, "mode", mode)
+    rng = np.random.default_rng(w.seed)
+    q, k, v, do = operands(rng, w.batch, w.length, w.q_heads, w.kv_heads, w.head_dim,
+                           torch.bfloat16, w.qkv_scale)
+    tm = torch.tensor(w.attention_mask, device=device)
+    ts = torch.tensor(w.segment_ids, device=device)
+    if mode == 0:
+        fn = lambda a, bb, c: attention.packed_causal_attention(a, bb, c, tm, ts, backend="dense")  # noqa: E731
+    else:
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = torch_reference(mode, q, k, v, w.attention_mask, w.segment_ids, do)
+    errs = {n: max_abs(a, r) for n, a, r in zip(("out", "dq", "dk", "dv"), got, ref)}
+    say(name, "max-abs", errs, "ref max |x|", {n: r.abs().max().item() for n, r in zip("o qkv", ref)})
+    for n, e in errs.items():
+        assert e < BF16_TOL, (n, e)
+
+
+def test_bf16_against_reference_cast_points(device):
+    """The reference's bf16 dense path (attention.py:23-33) emulated on the
+    CPU at a reduced packed shape; SDPA cast points for bidirectional."""
+    rng = np.random.default_rng(77)
+    b, t, hq, hkv = 2, 384, 4, 2
+    say("cast points", (b, t))
+    q, k, v, _ = operands(rng, b, t, hq, hkv, 64, torch.bfloat16, 0.5)
+    seg = np.repeat([[1, 2, 3, 4, 0]], [120, 64, 130, 60, 10], axis=1).repeat(b, 0).astype(np.int32)
+    mask = (seg != 0).astype(np.int32)
+    tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+    causal = attention.dense_packed_causal_attention(q, k, v, tm, ts).cpu()
+    bidir = bidirectional.attention(q, k, v, tm, ts).cpu()
+    valid, active = masks.packed_valid(mask, seg)
+    emu = oatt.dense_bf16_einsum(q.cpu(), k.cpu(), v.cpu(), torch.tensor(valid[:, None]))
+    emu = emu * torch.tensor(active[:, :, None, None]).to(emu.dtype)
+    assert max_abs(causal, emu) < BF16_TOL
+    bvalid, present = masks.bidirectional_valid(mask, seg)
+    emu = oatt.sdpa_bf16(q.cpu(), k.cpu(), v.cpu(), torch.tensor(bvalid[:, None]))
+    emu = torch.where(torch.tensor(present[:, :, None, None]), emu, torch.zeros((), dtype=emu.dtype))
+    assert max_abs(bidir, emu) < BF16_TOL
+
+
+def test_inactive_rows_are_exact_zero_even_with_nan_queries(device):
+    """bidirectional.py:31,35: inactive queries return exact 0."""
+    rng = np.random.default_rng(1)
+    say("nan inactive rows")
+    q, k, v, _ = operands(rng, 1, 200, 4, 2, 64, torch.bfloat16)
+    seg = np.repeat([[1, 0, 2, 0]], [60, 20, 100, 20], axis=1).astype(np.int32)
+    inactive = torch.tensor(seg == 0, device=device)
+    q[inactive] = float("nan")
+    ts = torch.tensor(seg, device=device)
+    out = bidirectional.attention(q, k, v, ts != 0, ts)
+    assert torch.isfinite(out).all()
+    assert (out[inactive] == 0).all()
+
+
+def test_all_padding_rows_and_single_token_segments(device):
+    rng = np.random.default_rng(2)
+    say("padding rows / single tokens")
+    q, k, v, do = operands(rng, 3, 130, 4, 2, 64, torch.float32)
+    seg = np.zeros((3, 130), np.int32)
+    seg[1] = np.arange(1, 131)          # every token its own segment
+    seg[2, :64] = 5
+    seg[2, 64:] = np.arange(66)         # repeated / mixed ids
+    ts = torch.tensor(seg, device=device)
+    for mode in (0, 1):
+        fn = (lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, ts != 0, ts)) \
+            if mode == 0 else (lambda a, bb, c: bidirectional.attention(a, bb, c, ts != 0, ts))
+        got = _grads(fn, q, k, v, do)
+        ref = oatt.grouped_fp64(mode, *(x.cpu().numpy() for x in (q, k, v)), seg != 0, seg,
+                                d_out=do.cpu().numpy())
+        for a, r in zip(got, ref):
+            np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5)
+        assert (got[0][0] == 0).all() and (got[3][0] == 0).all()
+
+
+def test_deterministic_bitwise(device):
+    w = packing.make_workload("C2")
+    say("determinism C2")
+    rng = np.random.default_rng(9)
+    q, k, v, do = operands(rng, w.batch, w.length, w.q_heads, w.kv_heads, 64, torch.bfloat16, 0.5)
+    tm = torch.tensor(w.attention_mask, device=device)
+    ts = torch.tensor(w.segment_ids, device=device)
+    fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    first = _grads(fn, q, k, v, do)
+    second = _grads(fn, q, k, v, do)
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+
+
+def test_head_dim_padding_path(device):
+    """D < 64 is served by zero-padding the head dim (exact)."""
+    rng = np.random.default_rng(4)
+    say("head dim 32")
+    q, k, v, do = operands(rng, 2, 100, 4, 2, 32, torch.float32)
+    seg = np.repeat([[1, 2, 0]], [40, 50, 10], axis=1).repeat(2, 0).astype(np.int32)
+    ts = torch.tensor(seg, device=device)
+    got = _grads(lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, ts != 0, ts),
+                 q, k, v, do)
+    ref = oatt.grouped_fp64(0, *(x.cpu().numpy() for x in (q, k, v)), seg != 0, seg,
+                            d_out=do.cpu().numpy())
+    for a, r in zip(got, ref):
+        np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError, match="head_dim"):
+        attention.dense_packed_causal_attention(
+            torch.zeros(1, 8, 2, 128, device=device), torch.zeros(1, 8, 2, 128, device=device),
+            torch.zeros(1, 8, 2, 128, device=device), ts[:1, :8] * 0 + 1, ts[:1, :8] * 0 + 1)

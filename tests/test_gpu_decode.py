@@ -1,0 +1,83 @@
+"""GPU parity of the ragged split-K decode (kernels/attention.py:264-282)."""
+
+import json
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import max_abs, say
+from mfattn.kernels import attention
+from oracle import attention as oatt
+from oracle import packing
+
+FIX = json.loads((pathlib.Path(__file__).parent / "golden" / "reference_fixtures.json").read_text())
+pytestmark = pytest.mark.gpu
+
+
+def test_reference_cached_fixture(device):
+    """tests/kernels/test_attention.py:377-398: seed 3, valid_length 4, D=8."""
+    dims = FIX["attention_dims"]
+    say("cached fixture")
+    rng = np.random.default_rng(dims["cached_seed"])
+    q, k, v = (rng.normal(size=s).astype(np.float32)
+               for s in [(2, 1, 4, 8), (2, 6, 2, 8), (2, 6, 2, 8)])
+    t = lambda x: torch.tensor(x, device=device)  # noqa: E731
+    out = attention.cached_attention(t(q), t(k), t(v), torch.tensor(4, dtype=torch.int32),
+                                     backend="dense")
+    ref = oatt.cached_fp64(q, k, v, np.array(4))[0]
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    assert out.shape == (2, 1, 4, 8)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ragged_lengths_and_edges(dtype, device):
+    rng = np.random.default_rng(5)
+    b, cap, hq, hkv = 7, 1000, 8, 2
+    say("decode ragged", dtype)
+    lengths = np.array([1, 999, 1000, 1500, 0, 257, 128], np.int32)
+    q = rng.standard_normal((b, 1, hq, 64)).astype(np.float32)
+    k = rng.standard_normal((b, cap, hkv, 64)).astype(np.float32)
+    v = rng.standard_normal((b, cap, hkv, 64)).astype(np.float32)
+    t = lambda x: torch.tensor(x, device=device).to(dtype)  # noqa: E731
+    out = attention.dense_cached_attention(t(q), t(k), t(v), torch.tensor(lengths, device=device))
+    qq, kk, vv = (t(x).float().cpu().numpy() for x in (q, k, v))
+    ref = oatt.cached_fp64(qq, kk, vv, lengths)[0]
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, rtol=tol, atol=tol)
+
+
+def test_c4_full_shape(device):
+    d = packing.make_decode_workload("C4")
+    say("C4 full")
+    rng = np.random.default_rng(d.seed)
+    g = torch.Generator(device="cpu").manual_seed(d.seed)
+    q = torch.randn(d.batch, 1, d.q_heads, d.head_dim, generator=g).to(device, torch.bfloat16)
+    k = torch.randn(d.batch, d.capacity, d.kv_heads, d.head_dim, generator=g).to(device, torch.bfloat16)
+    v = torch.randn(d.batch, d.capacity, d.kv_heads, d.head_dim, generator=g).to(device, torch.bfloat16)
+    lengths = torch.tensor(d.valid_length, device=device)
+    out = attention.cached_attention(q, k, v, lengths, backend="cudnn")
+    ref = torch.empty(d.batch, 1, d.q_heads, d.head_dim, device=device)
+    group = d.q_heads // d.kv_heads
+    for row in range(d.batch):
+        n = int(d.valid_length[row])
+        kk = k[row, :n].float().repeat_interleave(group, dim=1).permute(1, 0, 2).contiguous()
+        vv = v[row, :n].float().repeat_interleave(group, dim=1).permute(1, 0, 2).contiguous()
+        qq = q[row, 0].float()[:, None, :].contiguous()
+        p = torch.softmax(torch.matmul(qq, kk.transpose(1, 2).contiguous()) * 0.125, dim=-1)
+        ref[row, 0] = torch.matmul(p, vv)[:, 0]
+    err = max_abs(out, ref)
+    say("C4 max-abs", err)
+    assert err < 2e-2
+    del rng
+
+
+def test_scalar_length_broadcasts_and_backends_agree(device):
+    rng = np.random.default_rng(8)
+    say("scalar length")
+    q = torch.tensor(rng.standard_normal((3, 1, 4, 64)), dtype=torch.float32, device=device)
+    k = torch.tensor(rng.standard_normal((3, 50, 2, 64)), dtype=torch.float32, device=device)
+    a = attention.cached_attention(q, k, k, 17, backend="dense")
+    b = attention.cached_attention(q, k, k, torch.full((3,), 17, dtype=torch.int32), backend="cudnn")
+    assert torch.equal(a, b)
