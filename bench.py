@@ -1,0 +1,271 @@
+"""Benchmark of the packed-attention hot path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+* step = one pass of the hot path over the C2 batch (LFM2.5-350M encoder
+  shape: 8 rows x 4096 tokens, packed bidirectional attention, 16/8 heads,
+  D=64, bf16): block map + flash forward + the three backward launches, with
+  q/k/v/dO resident in HBM.  ``value`` = useful fwd+bwd TFLOP/s
+  (12 * D * Hq * useful pairs per step / time).
+* ``roofline`` = the dominant kernel of the step (largest average launch
+  duration, timed with HIP events on the launch stream) against the bf16 MFMA
+  peak; ``traffic`` comes from the committed rocprofv3 PMC summary when one
+  exists for that kernel and workload, else null.
+* ``decode`` = the C4 ragged KV-cached decode (64 x 1 token, cache lengths
+  U[128, 8192]): algorithmic HBM GB/s and its roofline fraction.
+* ``cpu_baseline`` = the reference's dense bidirectional path restated in
+  torch on the host cores (XLA-SDPA cast points: fp32 logits, bf16
+  probabilities; fwd + autograd bwd), timed per (row, KV-group) chunk of the
+  same C2 batch for about ``--cpu-seconds`` and scaled to useful TFLOP/s.
+
+Only one GPU is used; ``--gpus`` above 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "minifield-training_amd"))
+sys.path.insert(0, str(ROOT))
+
+METRIC = "packed GQA attn fwd+bwd useful TFLOP/s @350M shape; ragged decode HBM GB/s"
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+HBM_PEAK_GBPS = 8000.0
+
+
+def _events(n):
+    import torch
+
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def _time_calls(fn, iters):
+    """Average ms of ``fn`` (stream-ordered launches) with events around each call."""
+    import torch
+
+    starts, ends = _events(iters), _events(iters)
+    for i in range(iters):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / iters
+
+
+def _traffic(kernel: str, workload: str):
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    data = json.loads(path.read_text())
+    return data.get(workload, {}).get(kernel)
+
+
+def gpu_leg(steps: int, warmup: int):
+    import numpy as np
+    import torch
+
+    from mfattn import _lib, ops, workloads
+
+    dev = torch.device("cuda:0")
+    w = workloads.packed("C2")
+    mode = _lib.MODE_PACKED_CAUSAL if w.causal else _lib.MODE_PACKED_BIDIR
+    rng = np.random.default_rng(w.seed)
+
+    def mk(shape, scale):
+        return torch.tensor(rng.standard_normal(shape).astype(np.float32) * scale, device=dev).to(torch.bfloat16)
+
+    q = mk((w.batch, w.length, w.q_heads, w.head_dim), w.qkv_scale)
+    k = mk((w.batch, w.length, w.kv_heads, w.head_dim), w.qkv_scale)
+    v = mk((w.batch, w.length, w.kv_heads, w.head_dim), w.qkv_scale)
+    do = mk((w.batch, w.length, w.q_heads, w.head_dim), 1.0)
+    mask = torch.tensor(w.attention_mask, device=dev)
+    seg = torch.tensor(w.segment_ids, device=dev)
+    scale = w.head_dim ** -0.5
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = ops.bwd_workspace(q)
+
+    def step():
+        plan = ops.block_map(seg, mask, mode, w.length, w.length)
+        out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
+        ops.attn_bwd_delta(out, do, ws)
+        ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, scale, ws, dq)
+        ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    start, end = _events(2)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ms = start.elapsed_time(end) / steps
+
+    # per-kernel durations (HIP events on the launch stream)
+    plan = ops.block_map(seg, mask, mode, w.length, w.length)
+    out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
+    ops.attn_bwd_delta(out, do, ws)
+    torch.cuda.synchronize()
+    iters = max(steps, 5)
+    kern = {
+        "block_map": _time_calls(lambda: ops.block_map(seg, mask, mode, w.length, w.length), iters),
+        "attn_fwd": _time_calls(lambda: ops.attn_fwd(q, k, v, plan, mode, scale), iters),
+        "attn_bwd_delta": _time_calls(lambda: ops.attn_bwd_delta(out, do, ws), iters),
+        "attn_bwd_dq": _time_calls(lambda: ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, scale, ws, dq), iters),
+        "attn_bwd_dkdv": _time_calls(
+            lambda: ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv), iters),
+    }
+    flops = workloads.attention_flops(w)
+    algo = {"attn_fwd": flops["fwd"], "attn_bwd_dq": flops["dq"], "attn_bwd_dkdv": flops["dkdv"]}
+    dominant = max(algo, key=lambda name: kern[name])
+    achieved = algo[dominant] / (kern[dominant] * 1e-3) / 1e12
+    value = flops["fwd_bwd"] / (ms * 1e-3) / 1e12
+    result = {
+        "value": value,
+        "ms_per_step": ms,
+        "wall_ms_per_step": wall_ms,
+        "config": {"workload": w.description, "global_batch": w.batch, "seq_len": w.length,
+                   "q_heads": w.q_heads, "kv_heads": w.kv_heads, "head_dim": w.head_dim,
+                   "useful_pairs_per_head": workloads.useful_pairs(w.segment_ids, w.causal),
+                   "useful_gflop_per_step": flops["fwd_bwd"] / 1e9, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "kernel": dominant, "achieved": achieved,
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
+                     "traffic": _traffic(dominant, "C2"),
+                     "algorithmic_gflop_per_launch": algo[dominant] / 1e9},
+        "fa2_convention_tflops": flops["fwd_bwd_fa2"] / (ms * 1e-3) / 1e12,
+        "step_roofline_frac": (flops["fwd_bwd"] / (MFMA_BF16_PEAK_TFLOPS * 1e12)) / (ms * 1e-3),
+        "kernels_ms": kern,
+    }
+    del q, k, v, do, dq, dk, dv, out, lse, plan, ws
+    torch.cuda.empty_cache()
+    result["decode"] = decode_leg(steps, warmup)
+    return result
+
+
+def decode_leg(steps: int, warmup: int):
+    import torch
+
+    from mfattn import ops, workloads
+
+    dev = torch.device("cuda:0")
+    d = workloads.decode("C4")
+    g = torch.Generator(device=dev).manual_seed(d.seed)
+    shape_q = (d.batch, 1, d.q_heads, d.head_dim)
+    shape_c = (d.batch, d.capacity, d.kv_heads, d.head_dim)
+    q = torch.randn(shape_q, generator=g, device=dev).to(torch.bfloat16)
+    kc = torch.randn(shape_c, generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn(shape_c, generator=g, device=dev).to(torch.bfloat16)
+    lengths = torch.tensor(d.valid_length, device=dev)
+    scale = d.head_dim ** -0.5
+    run = lambda: ops.decode(q, kc, vc, lengths, scale)  # noqa: E731
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    iters = max(steps, 10)
+    ms = _time_calls(run, iters)
+    nbytes = workloads.decode_bytes(d)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"metric": "ragged decode HBM GB/s", "value": gbps, "unit": "GB/s", "us_per_step": ms * 1e3,
+            "workload": d.description, "algorithmic_bytes": nbytes,
+            "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": gbps / HBM_PEAK_GBPS, "traffic": _traffic("decode", "C4")}}
+
+
+def cpu_leg(seconds: float):
+    """Dense reference path on the host, per (row, KV-group) chunk of C2."""
+    import numpy as np
+    import torch
+
+    from mfattn import workloads
+    from oracle import attention as oatt
+    from oracle import masks as omasks
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    w = workloads.packed("C2")
+    g = w.q_heads // w.kv_heads
+    rng = np.random.default_rng(w.seed)
+    done_flops, elapsed, chunks = 0, 0.0, 0
+    total_chunks = w.batch * w.kv_heads
+    for row in range(w.batch):
+        valid, present = omasks.bidirectional_valid(w.attention_mask[row : row + 1],
+                                                    w.segment_ids[row : row + 1])
+        valid_t = torch.tensor(valid[:, None])
+        present_t = torch.tensor(present[:, :, None, None])
+        pairs = workloads.useful_pairs(w.segment_ids[row : row + 1], w.causal)
+        for _ in range(w.kv_heads):
+            mk = lambda h: torch.tensor(  # noqa: E731
+                rng.standard_normal((1, w.length, h, w.head_dim)).astype(np.float32) * w.qkv_scale
+            ).to(torch.bfloat16).requires_grad_(True)
+            q, k, v = mk(g), mk(1), mk(1)
+            do = torch.randn(1, w.length, g, w.head_dim).to(torch.bfloat16)
+            t0 = time.perf_counter()
+            out = oatt.sdpa_bf16(q, k, v, valid_t)
+            out = torch.where(present_t, out, torch.zeros((), dtype=out.dtype))
+            out.backward(do)
+            elapsed += time.perf_counter() - t0
+            done_flops += 12 * w.head_dim * g * pairs
+            chunks += 1
+            if elapsed >= seconds:
+                break
+        if elapsed >= seconds:
+            break
+    return {"value": done_flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{chunks} of {total_chunks} (row, KV-group) chunks of C2 in {elapsed:.1f} s; "
+                      "dense bidirectional attention with XLA-SDPA cast points (fp32 logits, bf16 "
+                      "probabilities) restated in torch-CPU, forward + autograd backward; useful "
+                      "FLOPs of the chunks / time"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
+              "(the packed-attention path has no cross-GPU work in this build)", file=sys.stderr)
+        return 2
+    gpu = gpu_leg(args.steps, args.warmup)
+    line = {
+        "metric": METRIC,
+        "value": gpu["value"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": gpu["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded packed C2 layout, q/k/v ~ 0.5 N(0,1), dO ~ N(0,1))",
+        "config": gpu["config"],
+        "roofline": gpu["roofline"],
+        "cpu_baseline": None if args.no_cpu_baseline else cpu_leg(args.cpu_seconds),
+        "decode": gpu["decode"],
+        "kernels_ms": gpu["kernels_ms"],
+        "fa2_convention_tflops": gpu["fa2_convention_tflops"],
+        "step_roofline_frac": gpu["step_roofline_frac"],
+        "wall_ms_per_step": gpu["wall_ms_per_step"],
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

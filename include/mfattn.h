@@ -106,6 +106,28 @@ int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                 void* dq, void* dk, void* dv, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* The three launches of mf_attn_bwd as separate entry points, for callers
+ * that schedule them themselves (e.g. dq and dk/dv on two streams) and for
+ * per-kernel timing.  mf_attn_bwd_delta writes rowsum(dO * O) into the
+ * workspace; mf_attn_bwd_dq and mf_attn_bwd_dkdv read it, so both must be
+ * ordered after it.  Arguments mean what they mean in mf_attn_bwd. */
+int mf_attn_bwd_delta(const void* out, const void* dout, int dtype, int batch,
+                      int q_len, int q_heads, int head_dim, void* workspace,
+                      size_t workspace_bytes, void* stream);
+int mf_attn_bwd_dq(const void* q, const void* k, const void* v,
+                   const void* dout, const float* lse, int dtype, int batch,
+                   int q_len, int kv_len, int q_heads, int kv_heads,
+                   int head_dim, int mode, float scale, const void* plan,
+                   size_t plan_bytes, void* dq, const void* workspace,
+                   size_t workspace_bytes, void* stream);
+int mf_attn_bwd_dkdv(const void* q, const void* k, const void* v,
+                     const void* dout, const float* lse, int dtype, int batch,
+                     int q_len, int kv_len, int q_heads, int kv_heads,
+                     int head_dim, int mode, float scale, const void* plan,
+                     size_t plan_bytes, void* dk, void* dv,
+                     const void* workspace, size_t workspace_bytes,
+                     void* stream);
+
 /* Ragged KV-cached decode.  Replaces dense_cached_attention
  * (kernels/attention.py:264-282) / cudnn_cached_attention (:366-396): one
  * query token per row attends to cache slots [0, lengths[b]) of a

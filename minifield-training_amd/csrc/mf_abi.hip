@@ -19,7 +19,7 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
 hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                            const void* dout, const float* lse, bool f32, int batch, int T, int S,
                            int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
-                           void* dk, void* dv, float* delta, hipStream_t stream);
+                           void* dk, void* dv, float* delta, int phases, hipStream_t stream);
 size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk);
 int decode_chunk(bool f32);
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
@@ -141,23 +141,74 @@ size_t mf_attn_bwd_workspace_bytes(int batch, int q_len, int q_heads) {
   return sizeof(float) * (size_t)batch * q_len * q_heads;
 }
 
-int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
-                const float* lse, int dtype, int batch, int q_len, int kv_len, int q_heads,
-                int kv_heads, int head_dim, int mode, float scale, const void* plan,
-                size_t plan_bytes, void* dq, void* dk, void* dv, void* workspace,
-                size_t workspace_bytes, void* stream) {
+namespace {
+
+// Shared validation + launch of the backward phases (1 delta, 2 dq, 4 dkdv).
+int attn_bwd_phases(const void* q, const void* k, const void* v, const void* out,
+                    const void* dout, const float* lse, int dtype, int batch, int q_len,
+                    int kv_len, int q_heads, int kv_heads, int head_dim, int mode, float scale,
+                    const void* plan, size_t plan_bytes, void* dq, void* dk, void* dv,
+                    void* workspace, size_t workspace_bytes, int phases, void* stream,
+                    const char* what) {
   if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
     return rc;
-  if (!q || !k || !v || !out || !dout || !lse || !plan || !dq || !dk || !dv || !workspace)
-    return fail(MF_ERR_INVALID_ARGUMENT, "every tensor pointer and the workspace must be non-null");
+  const bool need_qkv = phases & 6;
+  if ((need_qkv && (!q || !k || !v || !lse || !plan)) || !dout || !workspace ||
+      ((phases & 1) && !out) || ((phases & 2) && !dq) || ((phases & 4) && (!dk || !dv)))
+    return fail(MF_ERR_INVALID_ARGUMENT, "%s: a required tensor pointer or the workspace is null",
+                what);
   const size_t need = mf_attn_bwd_workspace_bytes(batch, q_len, q_heads);
   if (workspace_bytes < need)
     return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
   return check_hip(mf::launch_attn_bwd(q, k, v, out, dout, lse, dtype == MF_DTYPE_F32, batch, q_len,
                                        kv_len, q_heads, kv_heads, mode, scale, plan, dq, dk, dv,
-                                       static_cast<float*>(workspace),
+                                       static_cast<float*>(workspace), phases,
                                        static_cast<hipStream_t>(stream)),
-                   "mf_attn_bwd launch");
+                   what);
+}
+
+}  // namespace
+
+int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                const float* lse, int dtype, int batch, int q_len, int kv_len, int q_heads,
+                int kv_heads, int head_dim, int mode, float scale, const void* plan,
+                size_t plan_bytes, void* dq, void* dk, void* dv, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  return attn_bwd_phases(q, k, v, out, dout, lse, dtype, batch, q_len, kv_len, q_heads, kv_heads,
+                         head_dim, mode, scale, plan, plan_bytes, dq, dk, dv, workspace,
+                         workspace_bytes, 7, stream, "mf_attn_bwd launch");
+}
+
+int mf_attn_bwd_delta(const void* out, const void* dout, int dtype, int batch, int q_len,
+                      int q_heads, int head_dim, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  // the delta phase reads no plan; validate it against a minimal one
+  return attn_bwd_phases(nullptr, nullptr, nullptr, out, dout, nullptr, dtype, batch, q_len, q_len,
+                         q_heads, 1, head_dim, MF_MODE_PACKED_BIDIR, 1.f, nullptr,
+                         mf::plan_layout(batch, q_len, q_len).total, nullptr, nullptr, nullptr,
+                         workspace, workspace_bytes, 1, stream, "mf_attn_bwd_delta launch");
+}
+
+int mf_attn_bwd_dq(const void* q, const void* k, const void* v, const void* dout,
+                   const float* lse, int dtype, int batch, int q_len, int kv_len, int q_heads,
+                   int kv_heads, int head_dim, int mode, float scale, const void* plan,
+                   size_t plan_bytes, void* dq, const void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  return attn_bwd_phases(q, k, v, nullptr, dout, lse, dtype, batch, q_len, kv_len, q_heads,
+                         kv_heads, head_dim, mode, scale, plan, plan_bytes, dq, nullptr, nullptr,
+                         const_cast<void*>(workspace), workspace_bytes, 2, stream,
+                         "mf_attn_bwd_dq launch");
+}
+
+int mf_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* dout,
+                     const float* lse, int dtype, int batch, int q_len, int kv_len, int q_heads,
+                     int kv_heads, int head_dim, int mode, float scale, const void* plan,
+                     size_t plan_bytes, void* dk, void* dv, const void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  return attn_bwd_phases(q, k, v, nullptr, dout, lse, dtype, batch, q_len, kv_len, q_heads,
+                         kv_heads, head_dim, mode, scale, plan, plan_bytes, nullptr, dk, dv,
+                         const_cast<void*>(workspace), workspace_bytes, 4, stream,
+                         "mf_attn_bwd_dkdv launch");
 }
 
 size_t mf_decode_workspace_bytes(int batch, int capacity, int q_heads, int head_dim) {

@@ -673,7 +673,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
 hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                            const void* dout, const float* lse, bool f32, int batch, int T, int S,
                            int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
-                           void* dk, void* dv, float* delta, hipStream_t stream) {
+                           void* dk, void* dv, float* delta, int phases, hipStream_t stream) {
   BwdArgs a;
   const PlanLayout lay = plan_layout(batch, T, S);
   const char* p = reinterpret_cast<const char*>(plan);
@@ -709,12 +709,15 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   a.scale_log2 = scale * kLog2e;
   const size_t rows = (size_t)batch * T * Hq;
   const unsigned dgrid = (unsigned)((rows + 255) / 256);
-  if (f32)
-    hipLaunchKernelGGL((bwd_delta_kernel<true>), dim3(dgrid), dim3(256), 0, stream, a, batch);
-  else
-    hipLaunchKernelGGL((bwd_delta_kernel<false>), dim3(dgrid), dim3(256), 0, stream, a, batch);
+  if (phases & 1) {
+    if (f32)
+      hipLaunchKernelGGL((bwd_delta_kernel<true>), dim3(dgrid), dim3(256), 0, stream, a, batch);
+    else
+      hipLaunchKernelGGL((bwd_delta_kernel<false>), dim3(dgrid), dim3(256), 0, stream, a, batch);
+  }
   const dim3 qgrid(batch * Hkv * a.hchunks, lay.nq);
-  if (f32) {
+  if (!(phases & 2)) {
+  } else if (f32) {
     if (hpw == 2)
       hipLaunchKernelGGL((bwd_dq_kernel<2, true>), qgrid, dim3(256), 0, stream, a);
     else
@@ -726,10 +729,12 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
       hipLaunchKernelGGL((bwd_dq_kernel<1, false>), qgrid, dim3(256), 0, stream, a);
   }
   const dim3 kgrid(batch * Hkv, lay.nk);
-  if (f32)
-    hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((bwd_dkdv_kernel<false>), kgrid, dim3(256), 0, stream, a);
+  if (phases & 4) {
+    if (f32)
+      hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((bwd_dkdv_kernel<false>), kgrid, dim3(256), 0, stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -3,7 +3,7 @@
 ``mfattn.kernels.attention`` and ``mfattn.kernels.bidirectional`` mirror the
 reference's kernel modules; ``mfattn.ops`` is the tensor-level C-ABI binding.
 Importing the package loads ``libmfattn.so`` and raises ``ImportError`` if it
-is missing (build with ``python -m mfattn.build``).
+is missing (build with ``python minifield-training_amd/mfattn/build.py``).
 """
 
 from . import _lib, ops

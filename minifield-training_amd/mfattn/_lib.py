@@ -42,6 +42,9 @@ EXPORTS = (
     "mf_attn_fwd",
     "mf_attn_bwd_workspace_bytes",
     "mf_attn_bwd",
+    "mf_attn_bwd_delta",
+    "mf_attn_bwd_dq",
+    "mf_attn_bwd_dkdv",
     "mf_decode_workspace_bytes",
     "mf_decode",
     "mf_last_error",
@@ -65,7 +68,7 @@ def _load() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise ImportError(
             f"mfattn native library missing: {LIB_PATH} (build it with "
-            "`python -m mfattn.build` from minifield-training_amd/)"
+            "`python minifield-training_amd/mfattn/build.py`)"
         )
     try:
         lib = ctypes.CDLL(str(LIB_PATH))
@@ -86,6 +89,14 @@ def _load() -> ctypes.CDLL:
     lib.mf_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                 f32, vp, sz, vp, vp, vp, vp, sz, vp]
     lib.mf_attn_bwd.restype = i32
+    lib.mf_attn_bwd_delta.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]
+    lib.mf_attn_bwd_delta.restype = i32
+    lib.mf_attn_bwd_dq.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
+                                   f32, vp, sz, vp, vp, sz, vp]
+    lib.mf_attn_bwd_dq.restype = i32
+    lib.mf_attn_bwd_dkdv.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
+                                     f32, vp, sz, vp, vp, vp, sz, vp]
+    lib.mf_attn_bwd_dkdv.restype = i32
     lib.mf_decode_workspace_bytes.argtypes = [i32, i32, i32, i32]
     lib.mf_decode_workspace_bytes.restype = sz
     lib.mf_decode.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]

@@ -1,6 +1,7 @@
 """Build ``libmfattn.so`` (the HIP kernels + C ABI) in-tree for gfx950.
 
-``python -m mfattn.build`` (from ``minifield-training_amd/``) or
+``python minifield-training_amd/mfattn/build.py`` (a plain script: importing the
+package needs the library it builds) or
 ``mfattn.build.build()``.  Every ``.hip`` file under ``csrc/`` is compiled
 with ``hipcc --offload-arch=gfx950`` into an object in ``csrc/_build`` and
 linked into ``mfattn/libmfattn.so``.  Packed-FP32 instructions are disabled

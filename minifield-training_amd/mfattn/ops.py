@@ -131,6 +131,39 @@ def attn_bwd(q, k, v, out, dout, lse, plan: Plan, mode: int, scale: float):
     return dq, dk, dv
 
 
+def bwd_workspace(q: torch.Tensor) -> torch.Tensor:
+    b, t, hq, _ = q.shape
+    return torch.empty(_lib.LIB.mf_attn_bwd_workspace_bytes(b, t, hq), dtype=torch.uint8,
+                       device=q.device)
+
+
+def attn_bwd_delta(out, dout, ws) -> None:
+    """Phase 1 of the backward: rowsum(dO * O) into ``ws``."""
+    b, t, hq, d = out.shape
+    _lib.check(_lib.LIB.mf_attn_bwd_delta(_ptr(out), _ptr(dout), dtype_code(out), b, t, hq, d,
+                                          _ptr(ws), ws.numel(), _stream(out.device)))
+
+
+def attn_bwd_dq(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, dq) -> None:
+    """Phase 2 of the backward: dq (reads the delta phase's ``ws``)."""
+    b, t, hq, d = q.shape
+    s, hkv = k.shape[1], k.shape[2]
+    _lib.check(_lib.LIB.mf_attn_bwd_dq(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse),
+                                       dtype_code(q), b, t, s, hq, hkv, d, mode, float(scale),
+                                       _ptr(plan.buf), plan.nbytes, _ptr(dq), _ptr(ws), ws.numel(),
+                                       _stream(q.device)))
+
+
+def attn_bwd_dkdv(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, dk, dv) -> None:
+    """Phase 3 of the backward: dk and dv (reads the delta phase's ``ws``)."""
+    b, t, hq, d = q.shape
+    s, hkv = k.shape[1], k.shape[2]
+    _lib.check(_lib.LIB.mf_attn_bwd_dkdv(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse),
+                                         dtype_code(q), b, t, s, hq, hkv, d, mode, float(scale),
+                                         _ptr(plan.buf), plan.nbytes, _ptr(dk), _ptr(dv), _ptr(ws),
+                                         ws.numel(), _stream(q.device)))
+
+
 def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
            lengths: torch.Tensor, scale: float) -> torch.Tensor:
     device = require_device(q, k_cache, v_cache, lengths)

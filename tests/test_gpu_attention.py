@@ -26,6 +26,16 @@ pytestmark = pytest.mark.gpu
 BF16_TOL = 2e-2
 
 
+def bf16_excess(a: torch.Tensor, r: torch.Tensor) -> float:
+    """Largest error beyond the bf16 storage rounding of the true value:
+    ``max(|a - r| - 2**-8 |r|)``.  The bar is ``< 2e-2``: max-abs 2e-2 at
+    unit scale, plus the half-ulp (at most 2**-8 relative) that any bf16
+    result of a value of that size carries, which alone exceeds 2e-2 once
+    |r| > 5 (gradients of the unscaled C3/C5 inputs reach |r| ~ 10)."""
+    a, r = a.float(), r.float()
+    return (a - r).abs().sub(r.abs() * 2.0 ** -8).max().item() if a.numel() else 0.0
+
+
 def _grads(fn, q, k, v, do):
     q, k, v = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
     out = fn(q, k, v)
@@ -141,7 +151,7 @@ def test_random_layouts_against_oracle(mode, dtype, device):
         if dtype == "float32":
             np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
         else:
-            assert np.abs(a.float().cpu().numpy() - r).max() < BF16_TOL, name
+            assert bf16_excess(a.cpu(), torch.tensor(r)) < BF16_TOL, name
 
 
 @pytest.mark.parametrize("hq, hkv", [(4, 4), (8, 2), (6, 2), (3, 1)])
@@ -176,9 +186,12 @@ def test_baseline_config_bf16_fwd_bwd(name, device):
         fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
     got = _grads(fn, q, k, v, do)
     ref = torch_reference(mode, q, k, v, w.attention_mask, w.segment_ids, do)
-    errs = {n: max_abs(a, r) for n, a, r in zip(("out", "dq", "dk", "dv"), got, ref)}
-    say(name, "max-abs", errs, "ref max |x|", {n: r.abs().max().item() for n, r in zip("o qkv", ref)})
-    for n, e in errs.items():
+    names = ("out", "dq", "dk", "dv")
+    errs = {n: max_abs(a, r) for n, a, r in zip(names, got, ref)}
+    excess = {n: bf16_excess(a, r) for n, a, r in zip(names, got, ref)}
+    say(name, "max-abs", errs, "beyond bf16 rounding", excess,
+        "ref max |x|", {n: r.abs().max().item() for n, r in zip(names, ref)})
+    for n, e in excess.items():
         assert e < BF16_TOL, (n, e)
 
 
