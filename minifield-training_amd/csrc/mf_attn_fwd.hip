@@ -365,6 +365,227 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 forward: one head per wave, 4*HPW waves per workgroup.
+//
+// Wave w serves head hc*HPW + w/4 of the KV group and queries
+// [qt*128 + 32 (w%4), +32).  All waves of the workgroup share each 64-key
+// step's K and V tiles in LDS (the GQA sharing); K and V stay in their
+// natural row-major layout and the V^T operand of O^T += V^T P^T is built
+// with two transposing LDS reads per MFMA.  Global loads run two steps
+// ahead in two register sets; LDS is double-buffered.  Rescaling of the
+// output accumulator is lazy: the running max used for the exponentials
+// only moves when the true max exceeds it by more than 8 in log2 units, so
+// P <= 2^8 and the final division by the row sum is unchanged.
+// ---------------------------------------------------------------------------
+
+struct FwdLdsB {
+  bf16 k[2][kStepK * kLdsRow];  // K [key][d]
+  bf16 v[2][kStepK * kLdsRow];  // V [key][d]
+  int kid[2][kStepK];
+};
+
+template <int HPW>
+struct FwdStageB {
+  static constexpr int kChunks = 4 / HPW;  // 16-byte chunks per thread per step
+  u32x4 r[kChunks];
+  int kid;
+};
+
+template <int HPW>
+__device__ __forceinline__ void fwdb_load(const FwdArgs& a, int b, int kvh, int kb,
+                                          FwdStageB<HPW>& st) {
+  constexpr int T = 256 * HPW;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < FwdStageB<HPW>::kChunks; ++i) {
+    const int u = tid + T * i;
+    const int row = (u & 511) >> 3, ch = u & 7;
+    const bf16* src = reinterpret_cast<const bf16*>(u < 512 ? a.k : a.v);
+    const int key = kb + row;
+    st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
+                        : u32x4{0, 0, 0, 0};
+  }
+  if (tid < kStepK) st.kid = a.kid[(size_t)b * a.tk_pad + kb + tid];
+}
+
+template <int HPW>
+__device__ __forceinline__ void fwdb_store(const FwdStageB<HPW>& st, FwdLdsB& lds, int buf) {
+  constexpr int T = 256 * HPW;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < FwdStageB<HPW>::kChunks; ++i) {
+    const int u = tid + T * i;
+    const int row = (u & 511) >> 3, ch = u & 7;
+    bf16* dst = (u < 512 ? lds.k[buf] : lds.v[buf]) + row * kLdsRow + ch * 8;
+    st_u32x4(dst, st.r[i]);
+  }
+  if (tid < kStepK) lds.kid[buf][tid] = st.kid;
+}
+
+template <int HPW>
+__global__ __launch_bounds__(256 * HPW) void attn_fwd_bf16_kernel(FwdArgs a) {
+  __shared__ FwdLdsB lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int hr = blockIdx.x;  // (b, kvh, head chunk)
+  const int b = hr / (a.Hkv * a.hchunks);
+  const int kvh = (hr / a.hchunks) % a.Hkv;
+  const int hc = hr % a.hchunks;
+  const int qt = blockIdx.y;
+  const int head = kvh * a.G + hc * HPW + (wave >> 2);
+  const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
+  const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
+  const bool qvalid = qpos < a.T;
+
+  bf16x8 qf[4];
+  {
+    const bf16* src = reinterpret_cast<const bf16*>(a.q) +
+                      (((size_t)b * a.T + qpos) * a.Hq + head) * kD + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (qvalid) {
+        qf[ks] = ld_bf16x8(src + ks * 16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[ks][e] = (bf16)0.f;
+      }
+    }
+  }
+
+  f32x16 oacc[2] = {zero16(), zero16()};
+  float m_used = kNegInf, l = 0.f;
+  const float c = a.scale_log2;
+  const float tau = 8.f / c;  // lag allowed between m_used and the true max (raw units)
+
+  const int count = a.qcnt[(size_t)b * a.nq + qt];
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
+  const int nsteps = count * (kTile / kStepK);
+  auto step_kb = [&](int s) { return (list[s >> 1] >> 2) * kTile + (s & 1) * kStepK; };
+
+  // per-lane addressing of the transposing V^T reads
+  const int tr_row = ((lane & 15) >> 2) + 4 * half;           // + 16-key block base (+8)
+  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);  // + 32 * d block
+
+  auto compute = [&](int step, int buf) {
+    const int entry = list[step >> 1];
+    const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
+    const bool partial = (entry & 3) == 1;
+    f32x16 s[2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      s[kb2] = zero16();
+      const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kLdsRow + 8 * half];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) s[kb2] = mfma32x32x16(ld_bf16x8(krow + ks * 16), qf[ks], s[kb2]);
+    }
+    if (partial) {
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
+          const int4 kids = *reinterpret_cast<const int4*>(&lds.kid[buf][kk0]);
+          const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool ok = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
+            s[kb2][g4 * 4 + i] = ok ? s[kb2][g4 * 4 + i] : kNegInf;
+          }
+        }
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[kb2][r], s[kb2][r + 1]));
+    mx = halves_max(mx);
+    const bool grow = mx > m_used + tau;
+    if (__any(grow)) {
+      const float mnew = grow ? mx : m_used;
+      // a lane that has seen no valid key yet (m_used = -inf) has l = 0 and
+      // O = 0; give it alpha = 0 rather than exp2(-inf - -inf) = NaN
+      const float alpha = m_used == kNegInf ? 0.f : fast_exp2((m_used - mnew) * c);
+      m_used = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        oacc[0][r] *= alpha;
+        oacc[1][r] *= alpha;
+      }
+    }
+    const float mc = m_used == kNegInf ? 0.f : m_used * c;
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb2][r] = fast_exp2(fmaf(s[kb2][r], c, -mc));
+      pf[kb2][0] = pack8(s[kb2], 0);
+      pf[kb2][1] = pack8(s[kb2], 8);
+#pragma unroll
+      for (int ks2 = 0; ks2 < 2; ++ks2) {
+        const u32x4 w = __builtin_bit_cast(u32x4, pf[kb2][ks2]);
+        l = add_bf16_pair(w[0], l);
+        l = add_bf16_pair(w[1], l);
+        l = add_bf16_pair(w[2], l);
+        l = add_bf16_pair(w[3], l);
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ++ks2) {
+          const bf16* base = &lds.v[buf][(kb2 * 32 + ks2 * 16 + tr_row) * kLdsRow + db * 32 + tr_col];
+          const u32x2 lo = lds_read_tr16(base);
+          const u32x2 hi = lds_read_tr16(base + 8 * kLdsRow);
+          const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
+          oacc[db] = mfma32x32x16(__builtin_bit_cast(bf16x8, w), pf[kb2][ks2], oacc[db]);
+        }
+  };
+
+  FwdStageB<HPW> st0, st1;
+  if (nsteps > 0) fwdb_load<HPW>(a, b, kvh, step_kb(0), st0);
+  if (nsteps > 1) fwdb_load<HPW>(a, b, kvh, step_kb(1), st1);
+  if (nsteps > 0) fwdb_store<HPW>(st0, lds, 0);
+  __syncthreads();
+  for (int step = 0; step < nsteps; step += 2) {
+    // even step: data in buffer 0; st1 holds step+1
+    if (step + 2 < nsteps) fwdb_load<HPW>(a, b, kvh, step_kb(step + 2), st0);
+    compute(step, 0);
+    if (step + 1 < nsteps) fwdb_store<HPW>(st1, lds, 1);
+    __syncthreads();
+    if (step + 1 >= nsteps) break;
+    // odd step: data in buffer 1; st0 holds step+2
+    if (step + 3 < nsteps) fwdb_load<HPW>(a, b, kvh, step_kb(step + 3), st1);
+    compute(step + 1, 1);
+    if (step + 2 < nsteps) fwdb_store<HPW>(st0, lds, 0);
+    __syncthreads();
+  }
+
+  const bool qactive = qvalid && myqid != 0;
+  const float lt = halves_sum(l);
+  const bool has = qactive && lt > 0.f;
+  const float inv = has ? 1.f / lt : 0.f;
+  if (qvalid) {
+    if (half == 0)
+      a.lse[((size_t)b * a.Hq + head) * a.T + qpos] = has ? fmaf(m_used, a.scale, __logf(lt)) : kPosInf;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d0 = db * 32 + 8 * g4 + 4 * half;
+        bf16x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (bf16)(has ? oacc[db][g4 * 4 + i] * inv : 0.f);
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.out) +
+                                   (((size_t)b * a.T + qpos) * a.Hq + head) * kD + d0) = o;
+      }
+  }
+}
+
 hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32, int batch,
                            int T, int S, int Hq, int Hkv, int mode, float scale,
                            const void* plan, void* out, float* lse, hipStream_t stream) {
@@ -402,9 +623,9 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
       hipLaunchKernelGGL((attn_fwd_kernel<1, true>), grid, dim3(256), 0, stream, a);
   } else {
     if (hpw == 2)
-      hipLaunchKernelGGL((attn_fwd_kernel<2, false>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_bf16_kernel<2>), grid, dim3(512), 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_fwd_kernel<1, false>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_bf16_kernel<1>), grid, dim3(256), 0, stream, a);
   }
   return hipGetLastError();
 }

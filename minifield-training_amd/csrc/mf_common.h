@@ -75,6 +75,24 @@ __device__ __forceinline__ float halves_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane j receives
+// element e (0..3) = halfword (j & 3) of the 8 bytes addressed by lane
+// (j >> 2) + 4e.  If lane i of the group addresses row base + (i >> 2),
+// column c0 + 4 (i & 3) of a row-major 16-bit tile, lane j receives rows
+// base .. base+3 of column c0 + j: a 4-deep k-slice of a transposed operand.
+typedef __fp16 f16x4_raw __attribute__((__vector_size__(4 * sizeof(__fp16))));
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+  typedef __attribute__((address_space(3))) f16x4_raw* lds_ptr;
+  const f16x4_raw r = __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_ptr)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// Sum of the two bf16 halves of w plus acc (v_dot2c_f32_bf16 against 1.0).
+__device__ __forceinline__ float add_bf16_pair(uint32_t w, float acc) {
+  const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, acc, false);
+}
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
