@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "mf_common.h"
+#include "mf_kvstep.h"
 
 namespace mf {
 
@@ -187,10 +188,10 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
   const int hr = blockIdx.x;
-  const int b = hr / (a.Hkv * a.hchunks);
-  const int kvh = (hr / a.hchunks) % a.Hkv;
-  const int hc = hr % a.hchunks;
-  const int qt = blockIdx.y;
+  const int b = uniform(hr / (a.Hkv * a.hchunks));
+  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  const int hc = uniform(hr % a.hchunks);
+  const int qt = uniform(blockIdx.y);
   const int qpos = qt * kTile + wave * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
   const bool qvalid = qpos < a.T;
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
     dqacc[j][1] = zero16();
   }
 
-  const int count = a.qcnt[(size_t)b * a.nq + qt];
+  const int count = ld_const(a.qcnt, b * a.nq + qt);
   const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
   const int nsteps = count * (kTile / kStep);
   const float c = a.scale_log2;
@@ -501,9 +502,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
-  const int b = blockIdx.x / a.Hkv;
-  const int kvh = blockIdx.x % a.Hkv;
-  const int kt = blockIdx.y;
+  const int b = uniform(blockIdx.x / a.Hkv);
+  const int kvh = uniform(blockIdx.x % a.Hkv);
+  const int kt = uniform(blockIdx.y);
   const int kpos = kt * kTile + wave * 32 + (lane & 31);
   const int mykid = a.kid[(size_t)b * a.tk_pad + kpos];
   const bool kvalid = kpos < a.S;
@@ -544,7 +545,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
   f32x16 dkacc[2], dvacc[2];
   dkacc[0] = dkacc[1] = dvacc[0] = dvacc[1] = zero16();
 
-  const int count = a.kcnt[(size_t)b * a.nk + kt];
+  const int count = ld_const(a.kcnt, b * a.nk + kt);
   const int* list = a.klist + ((size_t)b * a.nk + kt) * a.nq;
   const int niters = count * a.G * 2;
   const float c = a.scale_log2;
@@ -670,6 +671,368 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 dq: structure of the bf16 forward (one head per wave, 4*HPW waves,
+// K/V steps staged through LDS two steps ahead).  dQ^T += K^T dS^T takes its
+// K^T operand from the natural K tile through transposing LDS reads.
+// ---------------------------------------------------------------------------
+template <int HPW>
+__global__ __launch_bounds__(256 * HPW) void bwd_dq_bf16_kernel(BwdArgs a) {
+  __shared__ KvStepLds lds;
+  constexpr int T = 256 * HPW;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int hr = blockIdx.x;
+  const int b = uniform(hr / (a.Hkv * a.hchunks));
+  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  const int hc = uniform(hr % a.hchunks);
+  const int qt = uniform(blockIdx.y);
+  const int head = kvh * a.G + hc * HPW + (wave >> 2);
+  const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
+  const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
+  const bool qvalid = qpos < a.T;
+  const bool qactive = qvalid && myqid != 0;
+
+  bf16x8 qf[4], gf[4];
+  {
+    const size_t row = (((size_t)b * a.T + qpos) * a.Hq + head) * kD + 8 * half;
+    const bf16* qs = reinterpret_cast<const bf16*>(a.q) + row;
+    const bf16* gs = reinterpret_cast<const bf16*>(a.dout) + row;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (qvalid) {
+        qf[ks] = ld_bf16x8(qs + ks * 16);
+        gf[ks] = ld_bf16x8(gs + ks * 16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[ks][e] = gf[ks][e] = (bf16)0.f;
+      }
+    }
+  }
+  const size_t li = ((size_t)b * a.Hq + head) * a.T + qpos;
+  const float lse2 = qactive ? a.lse[li] * kLog2e : kPosInf;
+  const float dlt = qvalid ? a.delta[li] : 0.f;
+  drain_memory();
+  f32x16 dqacc[2] = {zero16(), zero16()};
+  const float c = a.scale_log2;
+
+  const int count = ld_const(a.qcnt, b * a.nq + qt);
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
+  const int nsteps = count * (kTile / kKvStep);
+  auto step_kb = [&](int s) { return (ld_const(list, s >> 1) >> 2) * kTile + (s & 1) * kKvStep; };
+  const int tr_row = tr_row_of(lane);
+  const int tr_col = tr_col_of(lane);
+  const int* kid_row = a.kid + (size_t)b * a.tk_pad;
+  const size_t kv_base = ((size_t)b * a.S * a.Hkv + kvh) * kD;
+  const size_t key_stride = (size_t)a.Hkv * kD;
+
+  auto compute = [&](int step, int buf) {
+    const int entry = ld_const(list, step >> 1);
+    const int kb = (entry >> 2) * kTile + (step & 1) * kKvStep;
+    const bool partial = (entry & 3) == 1;
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      f32x16 s = zero16(), dp = zero16();
+      const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kKvPitch + 8 * half];
+      const bf16* vrow = &lds.v[buf][(kb2 * 32 + (lane & 31)) * kKvPitch + 8 * half];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        s = mfma32x32x16(ld_bf16x8(krow + ks * 16), qf[ks], s);
+        dp = mfma32x32x16(ld_bf16x8(vrow + ks * 16), gf[ks], dp);
+      }
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        bool ok[4] = {true, true, true, true};
+        if (partial) {
+          const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
+          const int4 kids = *reinterpret_cast<const int4*>(&lds.kid[buf][kk0]);
+          const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ok[i] = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = g4 * 4 + i;
+          const float p = ok[i] ? fast_exp2(fmaf(s[r], c, -lse2)) : 0.f;
+          s[r] = p * (dp[r] - dlt);
+        }
+      }
+      const bf16x8 ds0 = pack8(s, 0), ds1 = pack8(s, 8);
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const int col = db * 32 + tr_col;
+        dqacc[db] = mfma32x32x16(tr_operand(lds.k[buf], kKvPitch, kb2 * 32 + tr_row, col), ds0, dqacc[db]);
+        dqacc[db] = mfma32x32x16(tr_operand(lds.k[buf], kKvPitch, kb2 * 32 + 16 + tr_row, col), ds1, dqacc[db]);
+      }
+    }
+  };
+
+  auto load = [&](int s, KvStepStage<T>& st) {
+    kvstep_load<T>(a.k, a.v, kid_row, kv_base, key_stride, a.S, step_kb(s), st);
+  };
+  KvStepStage<T> st0, st1;
+  if (nsteps > 0) {
+    load(0, st0);
+    load(min(1, nsteps - 1), st1);
+  }
+  if (nsteps > 0) kvstep_store<T>(st0, lds, 0);
+  __syncthreads();
+  for (int step = 0; step < nsteps; step += 2) {
+    load(min(step + 2, nsteps - 1), st0);  // unconditional: see the forward
+    compute(step, 0);
+    if (step + 1 < nsteps) kvstep_store<T>(st1, lds, 1);
+    __syncthreads();
+    if (step + 1 >= nsteps) break;
+    load(min(step + 3, nsteps - 1), st1);
+    compute(step + 1, 1);
+    if (step + 2 < nsteps) kvstep_store<T>(st0, lds, 0);
+    __syncthreads();
+  }
+
+  if (!qvalid) return;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = db * 32 + 8 * g4 + 4 * half;
+      bf16x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (bf16)(qactive ? dqacc[db][g4 * 4 + i] * a.scale : 0.f);
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dq) +
+                                 (((size_t)b * a.T + qpos) * a.Hq + head) * kD + d0) = o;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 dk/dv: 4*HS waves per workgroup for one 128-key tile of one KV head.
+// Waves w and w+4 own the same 32 keys (K, V as B operands in registers) and
+// process different query heads of the GQA group (slot w/4 takes heads
+// slot, slot+HS, ...), so each query step stages Q and dO of HS heads; their
+// dK/dV are summed through LDS at the end.  dV^T += dO^T P and dK^T += Q^T dS
+// read their transposed operands from the natural Q / dO tiles.
+// ---------------------------------------------------------------------------
+template <int HS>
+struct DkdvLds {
+  bf16 q[2][HS][kKvStep * kKvPitch];
+  bf16 g[2][HS][kKvStep * kKvPitch];
+  float lse2[2][HS][kKvStep];
+  float dlt[2][HS][kKvStep];
+  int qid[2][kKvStep];
+};
+
+template <int HS>
+struct DkdvStage {
+  u32x4 r[4];
+  float lse2, dlt;
+  int qid;
+};
+
+template <int HS>
+__global__ __launch_bounds__(256 * HS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
+  __shared__ DkdvLds<HS> lds;
+  constexpr int T = 256 * HS;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;
+  const int slot = wave >> 2;
+  const int b = uniform(blockIdx.x / a.Hkv);
+  const int kvh = uniform(blockIdx.x % a.Hkv);
+  const int kt = uniform(blockIdx.y);
+  const int kpos = kt * kTile + (wave & 3) * 32 + (lane & 31);
+  const int mykid = a.kid[(size_t)b * a.tk_pad + kpos];
+  const bool kvalid = kpos < a.S;
+
+  bf16x8 kf[4], vf[4];
+  {
+    const size_t row = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD + 8 * half;
+    const bf16* ks = reinterpret_cast<const bf16*>(a.k) + row;
+    const bf16* vs = reinterpret_cast<const bf16*>(a.v) + row;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (kvalid) {
+        kf[i] = ld_bf16x8(ks + i * 16);
+        vf[i] = ld_bf16x8(vs + i * 16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[i][e] = vf[i][e] = (bf16)0.f;
+      }
+    }
+  }
+  drain_memory();
+  f32x16 dkacc[2] = {zero16(), zero16()}, dvacc[2] = {zero16(), zero16()};
+
+  const int count = ld_const(a.kcnt, b * a.nk + kt);
+  const int* list = a.klist + ((size_t)b * a.nk + kt) * a.nq;
+  const int hps = a.G / HS;        // heads per slot
+  const int per_tile = hps * 2;    // (head, 64-query half) iterations per query tile
+  const int niters = count * per_tile;
+  const float c = a.scale_log2;
+  const int tr_row = tr_row_of(lane);
+  const int tr_col = tr_col_of(lane);
+
+  auto iter = [&](int it, int& qb, int& hj, int& cls) {
+    const int entry = ld_const(list, it / per_tile);
+    const int rem = it % per_tile;
+    hj = rem >> 1;
+    qb = (entry >> 2) * kTile + (rem & 1) * kKvStep;
+    cls = entry & 3;
+  };
+  auto load = [&](int it, DkdvStage<HS>& st) {
+    int qb, hj, cls;
+    iter(it, qb, hj, cls);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + T * i;           // (slot, tensor, row, chunk)
+      const int s = u >> 10, tensor = (u >> 9) & 1, row = (u & 511) >> 3, ch = u & 7;
+      const int h = kvh * a.G + s + HS * hj;
+      // rows past the end re-read the last row; their P is 0 (lse = +inf)
+      const int qq = min(qb + row, a.T - 1);
+      const bf16* src = reinterpret_cast<const bf16*>(tensor ? a.dout : a.q);
+      st.r[i] = ld_u32x4(src + (((size_t)b * a.T + qq) * a.Hq + h) * kD + ch * 8);
+    }
+    {
+      // every thread loads (clamped, in bounds) so no load sits in a branch
+      const int s = (tid >> 6) % HS, qq = qb + (tid & 63);
+      const int h = kvh * a.G + s + HS * hj;
+      const int id = a.qid[(size_t)b * a.tq_pad + qq];
+      const bool act = qq < a.T && id != 0;
+      const size_t li = ((size_t)b * a.Hq + h) * a.T + min(qq, a.T - 1);
+      const float lse = a.lse[li], dl = a.delta[li];
+      st.qid = id;
+      st.lse2 = act ? lse * kLog2e : kPosInf;
+      st.dlt = act ? dl : 0.f;
+    }
+  };
+  auto store = [&](const DkdvStage<HS>& st, int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = tid + T * i;
+      const int s = u >> 10, tensor = (u >> 9) & 1, row = (u & 511) >> 3, ch = u & 7;
+      st_u32x4((tensor ? lds.g[buf][s] : lds.q[buf][s]) + row * kKvPitch + ch * 8, st.r[i]);
+    }
+    if (tid < kKvStep * HS) {
+      const int s = tid >> 6, r = tid & 63;
+      lds.lse2[buf][s][r] = st.lse2;
+      lds.dlt[buf][s][r] = st.dlt;
+      if (s == 0) lds.qid[buf][r] = st.qid;
+    }
+  };
+
+  auto compute = [&](int it, int buf) {
+    int qb, hj, cls;
+    iter(it, qb, hj, cls);
+    const bool partial = cls == 1;
+    const bf16* qt = lds.q[buf][slot];
+    const bf16* gt = lds.g[buf][slot];
+#pragma unroll 1
+    for (int qb2 = 0; qb2 < 2; ++qb2) {
+      f32x16 s = zero16(), dp = zero16();
+      const bf16* qrow = qt + (qb2 * 32 + (lane & 31)) * kKvPitch + 8 * half;
+      const bf16* grow = gt + (qb2 * 32 + (lane & 31)) * kKvPitch + 8 * half;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        s = mfma32x32x16(ld_bf16x8(qrow + ks * 16), kf[ks], s);
+        dp = mfma32x32x16(ld_bf16x8(grow + ks * 16), vf[ks], dp);
+      }
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int qq0 = qb2 * 32 + 8 * g4 + 4 * half;
+        const float4 l4 = *reinterpret_cast<const float4*>(&lds.lse2[buf][slot][qq0]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&lds.dlt[buf][slot][qq0]);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+        bool ok[4] = {true, true, true, true};
+        if (partial) {
+          const int4 ids = *reinterpret_cast<const int4*>(&lds.qid[buf][qq0]);
+          const int iv[4] = {ids.x, ids.y, ids.z, ids.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ok[i] = iv[i] == mykid && (!a.causal || kpos <= qb + qq0 + i);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = g4 * 4 + i;
+          const float p = ok[i] ? fast_exp2(fmaf(s[r], c, -lv[i])) : 0.f;
+          s[r] = p;
+          dp[r] = p * (dp[r] - dv4[i]);
+        }
+      }
+      const bf16x8 pf0 = pack8(s, 0), pf1 = pack8(s, 8);
+      const bf16x8 sf0 = pack8(dp, 0), sf1 = pack8(dp, 8);
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const int col = db * 32 + tr_col;
+        const int r0 = qb2 * 32 + tr_row;
+        dvacc[db] = mfma32x32x16(tr_operand(gt, kKvPitch, r0, col), pf0, dvacc[db]);
+        dvacc[db] = mfma32x32x16(tr_operand(gt, kKvPitch, r0 + 16, col), pf1, dvacc[db]);
+        dkacc[db] = mfma32x32x16(tr_operand(qt, kKvPitch, r0, col), sf0, dkacc[db]);
+        dkacc[db] = mfma32x32x16(tr_operand(qt, kKvPitch, r0 + 16, col), sf1, dkacc[db]);
+      }
+    }
+  };
+
+  DkdvStage<HS> st0, st1;
+  if (niters > 0) {
+    load(0, st0);
+    load(min(1, niters - 1), st1);
+    store(st0, 0);
+  }
+  __syncthreads();
+  for (int it = 0; it < niters; it += 2) {
+    load(min(it + 2, niters - 1), st0);  // unconditional prefetch (see the forward)
+    compute(it, 0);
+    if (it + 1 < niters) store(st1, 1);
+    __syncthreads();
+    if (it + 1 >= niters) break;
+    load(min(it + 3, niters - 1), st1);
+    compute(it + 1, 1);
+    if (it + 2 < niters) store(st0, 0);
+    __syncthreads();
+  }
+
+  if constexpr (HS == 2) {
+    // slot 1 hands its partial dK/dV to slot 0 through LDS (staging is idle)
+    float* red = reinterpret_cast<float*>(&lds);
+    float* mine = red + ((wave & 3) * 64 + lane) * 64;
+    if (slot == 1) {
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          mine[db * 16 + r] = dkacc[db][r];
+          mine[32 + db * 16 + r] = dvacc[db][r];
+        }
+    }
+    __syncthreads();
+    if (slot == 1) return;
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        dkacc[db][r] += mine[db * 16 + r];
+        dvacc[db][r] += mine[32 + db * 16 + r];
+      }
+  }
+  if (!kvalid) return;
+  const bool kactive = mykid != 0;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = db * 32 + 8 * g4 + 4 * half;
+      const size_t off = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD + d0;
+      bf16x4 ok, ov;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ok[i] = (bf16)(kactive ? dkacc[db][g4 * 4 + i] * a.scale : 0.f);
+        ov[i] = (bf16)(kactive ? dvacc[db][g4 * 4 + i] : 0.f);
+      }
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dk) + off) = ok;
+      *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dv) + off) = ov;
+    }
+}
+
 hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                            const void* dout, const float* lse, bool f32, int batch, int T, int S,
                            int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
@@ -724,16 +1087,16 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
       hipLaunchKernelGGL((bwd_dq_kernel<1, true>), qgrid, dim3(256), 0, stream, a);
   } else {
     if (hpw == 2)
-      hipLaunchKernelGGL((bwd_dq_kernel<2, false>), qgrid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dq_bf16_kernel<2>), qgrid, dim3(512), 0, stream, a);
     else
-      hipLaunchKernelGGL((bwd_dq_kernel<1, false>), qgrid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dq_bf16_kernel<1>), qgrid, dim3(256), 0, stream, a);
   }
   const dim3 kgrid(batch * Hkv, lay.nk);
   if (phases & 4) {
     if (f32)
       hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);
     else
-      hipLaunchKernelGGL((bwd_dkdv_kernel<false>), kgrid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dkdv_bf16_kernel<1>), kgrid, dim3(256), 0, stream, a);
   }
   return hipGetLastError();
 }

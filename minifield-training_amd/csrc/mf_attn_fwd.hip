@@ -16,6 +16,7 @@
 #include <type_traits>
 
 #include "mf_common.h"
+#include "mf_kvstep.h"
 
 namespace mf {
 
@@ -146,10 +147,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
   const int hr = blockIdx.x;  // (b, kvh, head chunk)
-  const int b = hr / (a.Hkv * a.hchunks);
-  const int kvh = (hr / a.hchunks) % a.Hkv;
-  const int hc = hr % a.hchunks;
-  const int qt = blockIdx.y;
+  const int b = uniform(hr / (a.Hkv * a.hchunks));
+  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  const int hc = uniform(hr % a.hchunks);
+  const int qt = uniform(blockIdx.y);
   const int qpos = qt * kTile + wave * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
   const bool qvalid = qpos < a.T;
@@ -193,7 +194,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     l[j] = 0.f;
   }
 
-  const int count = a.qcnt[(size_t)b * a.nq + qt];
+  const int count = ld_const(a.qcnt, b * a.nq + qt);
   const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
   const int nsteps = count * (kTile / kStepK);
   const float c = a.scale_log2;
@@ -379,61 +380,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
 // P <= 2^8 and the final division by the row sum is unchanged.
 // ---------------------------------------------------------------------------
 
-struct FwdLdsB {
-  bf16 k[2][kStepK * kLdsRow];  // K [key][d]
-  bf16 v[2][kStepK * kLdsRow];  // V [key][d]
-  int kid[2][kStepK];
-};
-
-template <int HPW>
-struct FwdStageB {
-  static constexpr int kChunks = 4 / HPW;  // 16-byte chunks per thread per step
-  u32x4 r[kChunks];
-  int kid;
-};
-
-template <int HPW>
-__device__ __forceinline__ void fwdb_load(const FwdArgs& a, int b, int kvh, int kb,
-                                          FwdStageB<HPW>& st) {
-  constexpr int T = 256 * HPW;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < FwdStageB<HPW>::kChunks; ++i) {
-    const int u = tid + T * i;
-    const int row = (u & 511) >> 3, ch = u & 7;
-    const bf16* src = reinterpret_cast<const bf16*>(u < 512 ? a.k : a.v);
-    const int key = kb + row;
-    st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
-                        : u32x4{0, 0, 0, 0};
-  }
-  if (tid < kStepK) st.kid = a.kid[(size_t)b * a.tk_pad + kb + tid];
-}
-
-template <int HPW>
-__device__ __forceinline__ void fwdb_store(const FwdStageB<HPW>& st, FwdLdsB& lds, int buf) {
-  constexpr int T = 256 * HPW;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int i = 0; i < FwdStageB<HPW>::kChunks; ++i) {
-    const int u = tid + T * i;
-    const int row = (u & 511) >> 3, ch = u & 7;
-    bf16* dst = (u < 512 ? lds.k[buf] : lds.v[buf]) + row * kLdsRow + ch * 8;
-    st_u32x4(dst, st.r[i]);
-  }
-  if (tid < kStepK) lds.kid[buf][tid] = st.kid;
-}
-
 template <int HPW>
 __global__ __launch_bounds__(256 * HPW) void attn_fwd_bf16_kernel(FwdArgs a) {
-  __shared__ FwdLdsB lds;
+  __shared__ KvStepLds lds;
+  constexpr int T = 256 * HPW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
   const int hr = blockIdx.x;  // (b, kvh, head chunk)
-  const int b = hr / (a.Hkv * a.hchunks);
-  const int kvh = (hr / a.hchunks) % a.Hkv;
-  const int hc = hr % a.hchunks;
-  const int qt = blockIdx.y;
+  const int b = uniform(hr / (a.Hkv * a.hchunks));
+  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  const int hc = uniform(hr % a.hchunks);
+  const int qt = uniform(blockIdx.y);
   const int head = kvh * a.G + hc * HPW + (wave >> 2);
   const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
@@ -454,29 +412,32 @@ __global__ __launch_bounds__(256 * HPW) void attn_fwd_bf16_kernel(FwdArgs a) {
     }
   }
 
+  drain_memory();
   f32x16 oacc[2] = {zero16(), zero16()};
   float m_used = kNegInf, l = 0.f;
   const float c = a.scale_log2;
   const float tau = 8.f / c;  // lag allowed between m_used and the true max (raw units)
 
-  const int count = a.qcnt[(size_t)b * a.nq + qt];
+  const int count = ld_const(a.qcnt, b * a.nq + qt);
   const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
   const int nsteps = count * (kTile / kStepK);
-  auto step_kb = [&](int s) { return (list[s >> 1] >> 2) * kTile + (s & 1) * kStepK; };
+  auto step_kb = [&](int s) { return (ld_const(list, s >> 1) >> 2) * kTile + (s & 1) * kStepK; };
 
-  // per-lane addressing of the transposing V^T reads
-  const int tr_row = ((lane & 15) >> 2) + 4 * half;           // + 16-key block base (+8)
-  const int tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);  // + 32 * d block
+  const int tr_row = tr_row_of(lane);
+  const int tr_col = tr_col_of(lane);
+  const int* kid_row = a.kid + (size_t)b * a.tk_pad;
+  const size_t kv_base = ((size_t)b * a.S * a.Hkv + kvh) * kD;
+  const size_t key_stride = (size_t)a.Hkv * kD;
 
   auto compute = [&](int step, int buf) {
-    const int entry = list[step >> 1];
+    const int entry = ld_const(list, step >> 1);
     const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
     const bool partial = (entry & 3) == 1;
     f32x16 s[2];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
       s[kb2] = zero16();
-      const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kLdsRow + 8 * half];
+      const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kKvPitch + 8 * half];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) s[kb2] = mfma32x32x16(ld_bf16x8(krow + ks * 16), qf[ks], s[kb2]);
     }
@@ -538,30 +499,35 @@ __global__ __launch_bounds__(256 * HPW) void attn_fwd_bf16_kernel(FwdArgs a) {
       for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
         for (int ks2 = 0; ks2 < 2; ++ks2) {
-          const bf16* base = &lds.v[buf][(kb2 * 32 + ks2 * 16 + tr_row) * kLdsRow + db * 32 + tr_col];
-          const u32x2 lo = lds_read_tr16(base);
-          const u32x2 hi = lds_read_tr16(base + 8 * kLdsRow);
-          const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
-          oacc[db] = mfma32x32x16(__builtin_bit_cast(bf16x8, w), pf[kb2][ks2], oacc[db]);
+          const bf16x8 vt = tr_operand(lds.v[buf], kKvPitch, kb2 * 32 + ks2 * 16 + tr_row, db * 32 + tr_col);
+          oacc[db] = mfma32x32x16(vt, pf[kb2][ks2], oacc[db]);
         }
   };
 
-  FwdStageB<HPW> st0, st1;
-  if (nsteps > 0) fwdb_load<HPW>(a, b, kvh, step_kb(0), st0);
-  if (nsteps > 1) fwdb_load<HPW>(a, b, kvh, step_kb(1), st1);
-  if (nsteps > 0) fwdb_store<HPW>(st0, lds, 0);
+  auto load = [&](int s, KvStepStage<T>& st) {
+    kvstep_load<T>(a.k, a.v, kid_row, kv_base, key_stride, a.S, step_kb(s), st);
+  };
+  KvStepStage<T> st0, st1;
+  if (nsteps > 0) {
+    load(0, st0);
+    load(min(1, nsteps - 1), st1);
+  }
+  if (nsteps > 0) kvstep_store<T>(st0, lds, 0);
   __syncthreads();
+  // Prefetches are issued unconditionally (clamped to the last step, a
+  // harmless re-read) so the number of loads in flight is fixed and the
+  // wait before each LDS store covers only the older stage.
   for (int step = 0; step < nsteps; step += 2) {
     // even step: data in buffer 0; st1 holds step+1
-    if (step + 2 < nsteps) fwdb_load<HPW>(a, b, kvh, step_kb(step + 2), st0);
+    load(min(step + 2, nsteps - 1), st0);
     compute(step, 0);
-    if (step + 1 < nsteps) fwdb_store<HPW>(st1, lds, 1);
+    if (step + 1 < nsteps) kvstep_store<T>(st1, lds, 1);
     __syncthreads();
     if (step + 1 >= nsteps) break;
     // odd step: data in buffer 1; st0 holds step+2
-    if (step + 3 < nsteps) fwdb_load<HPW>(a, b, kvh, step_kb(step + 3), st1);
+    load(min(step + 3, nsteps - 1), st1);
     compute(step + 1, 1);
-    if (step + 2 < nsteps) fwdb_store<HPW>(st0, lds, 0);
+    if (step + 2 < nsteps) kvstep_store<T>(st0, lds, 0);
     __syncthreads();
   }
 

@@ -124,6 +124,26 @@ __device__ __forceinline__ void st_u32x2(void* p, const u32x2& v) {
   *reinterpret_cast<u32x2*>(p) = v;
 }
 
+// A wave-uniform integer forced into a scalar register.  Index arithmetic
+// on blockIdx with runtime divisors is lowered through VALU; without this the
+// dependent loads become vector loads and the work loops become divergent.
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Read of a wave-uniform index from memory that is immutable for the whole
+// kernel (the plan's work lists): the constant address space lets the
+// compiler use a scalar load, which does not queue behind the vector loads
+// in flight.
+__device__ __forceinline__ int ld_const(const int* p, int i) {
+  return ((const __attribute__((address_space(4))) int*)(p))[__builtin_amdgcn_readfirstlane(i)];
+}
+
+// Wait for every outstanding memory operation.  Used once, after the
+// per-wave operands that stay in registers for the whole kernel are loaded:
+// the compiler's wait insertion cannot see across the work loop's back edge
+// that those loads completed, and would otherwise wait for all in-flight
+// prefetches at the top of every step.
+__device__ __forceinline__ void drain_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Mask element: nonzero means active.
 __device__ __forceinline__ int mask_at(const void* mask, int mask_u8, long idx) {
   return mask_u8 ? (int)reinterpret_cast<const uint8_t*>(mask)[idx]

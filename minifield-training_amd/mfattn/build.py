@@ -30,6 +30,9 @@ FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # min/max need no NaN quieting: masked scores are -inf, never NaN
+    "-fno-honor-nans",
+    "-mno-amdgpu-ieee",
     "-Wall",
     "-Wno-unused-function",
 ]
