@@ -17,6 +17,7 @@
 
 #include "mf_common.h"
 #include "mf_kvstep.h"
+#include "mf_lds.h"
 
 namespace mf {
 
@@ -371,21 +372,47 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
 //
 // Wave w serves head hc*HPW + w/4 of the KV group and queries
 // [qt*128 + 32 (w%4), +32).  All waves of the workgroup share each 64-key
-// step's K and V tiles in LDS (the GQA sharing); K and V stay in their
-// natural row-major layout and the V^T operand of O^T += V^T P^T is built
-// with two transposing LDS reads per MFMA.  Global loads run two steps
-// ahead in two register sets; LDS is double-buffered.  Rescaling of the
-// output accumulator is lazy: the running max used for the exponentials
-// only moves when the true max exceeds it by more than 8 in log2 units, so
-// P <= 2^8 and the final division by the row sum is unchanged.
+// step's K and V tiles (the GQA sharing).  The tiles are DMA'd from HBM into a
+// three-stage LDS ring two steps ahead of use (no staging registers); K feeds
+// the S^T = K Q^T MFMAs directly and V^T is read with transposing LDS reads.
+// Rescaling of the output accumulator is lazy: the running max used for the
+// exponentials only moves when the true max exceeds it by more than 8 in
+// log2 units, so P <= 2^8 and the final division by the row sum is
+// unchanged.  Row sums are fp32 adds (v_dot2 would occupy the matrix pipe).
 // ---------------------------------------------------------------------------
+constexpr int kStageBytes = 2 * kTileBytes + 256;  // K tile, V tile, 64 key ids
+
+template <int W>
+struct KvDma {
+  static constexpr int kGroups = 8 / W;            // 8-row groups per tile per wave
+  static constexpr int kIds = 64 / W;              // key ids per wave
+  static constexpr int kPerStep = 2 * kGroups + 1; // DMA instructions per wave per step
+};
+
+// DMA of keys kb .. kb+63 (K rows, V rows, canonical ids) into one stage.
+template <int W>
+__device__ __forceinline__ void kv_dma(const char* kg, const char* vg, size_t row_stride, int S,
+                                       const int* kid_row, int kb, int wave, char* stage) {
+#pragma unroll
+  for (int j = 0; j < KvDma<W>::kGroups; ++j) {
+    const int r0 = 8 * (wave + W * j);
+    dma_rows8(kg, row_stride, kb, r0, S - 1, stage);
+    dma_rows8(vg, row_stride, kb, r0, S - 1, stage + kTileBytes);
+  }
+  constexpr int E = KvDma<W>::kIds;
+  dma_words(kid_row + kb + E * wave, stage + 2 * kTileBytes + 4 * E * wave, E);
+}
 
 template <int HPW>
-__global__ __launch_bounds__(256 * HPW) void attn_fwd_bf16_kernel(FwdArgs a) {
-  __shared__ KvStepLds lds;
-  constexpr int T = 256 * HPW;
+__global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2 * HPW)))
+void attn_fwd_bf16_kernel(FwdArgs a) {
+  constexpr int W = 4 * HPW;
+  __shared__ __attribute__((aligned(16))) char stage0[kStageBytes], stage1[kStageBytes],
+      stage2[kStageBytes];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // scalar wave index: keeps the DMA destinations scalar expressions of the
+  // stage arrays, so the compiler sees which stage each DMA writes
+  const int wave = uniform(threadIdx.x >> 6);
   const int half = lane >> 5;
   const int hr = blockIdx.x;  // (b, kvh, head chunk)
   const int b = uniform(hr / (a.Hkv * a.hchunks));
@@ -400,19 +427,12 @@ __global__ __launch_bounds__(256 * HPW) void attn_fwd_bf16_kernel(FwdArgs a) {
   bf16x8 qf[4];
   {
     const bf16* src = reinterpret_cast<const bf16*>(a.q) +
-                      (((size_t)b * a.T + qpos) * a.Hq + head) * kD + 8 * half;
+                      (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (qvalid) {
-        qf[ks] = ld_bf16x8(src + ks * 16);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[ks][e] = (bf16)0.f;
-      }
-    }
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = ld_bf16x8(src + ks * 16);
   }
-
   drain_memory();
+
   f32x16 oacc[2] = {zero16(), zero16()};
   float m_used = kNegInf, l = 0.f;
   const float c = a.scale_log2;
@@ -422,114 +442,101 @@ __global__ __launch_bounds__(256 * HPW) void attn_fwd_bf16_kernel(FwdArgs a) {
   const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
   const int nsteps = count * (kTile / kStepK);
   auto step_kb = [&](int s) { return (ld_const(list, s >> 1) >> 2) * kTile + (s & 1) * kStepK; };
-
   const int tr_row = tr_row_of(lane);
   const int tr_col = tr_col_of(lane);
   const int* kid_row = a.kid + (size_t)b * a.tk_pad;
-  const size_t kv_base = ((size_t)b * a.S * a.Hkv + kvh) * kD;
-  const size_t key_stride = (size_t)a.Hkv * kD;
+  const size_t row_stride = (size_t)a.Hkv * kD * sizeof(bf16);
+  const char* kg = reinterpret_cast<const char*>(a.k) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
+  const char* vg = reinterpret_cast<const char*>(a.v) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
 
-  auto compute = [&](int step, int buf) {
+  auto issue = [&](int s, char* stage) {
+    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage);
+  };
+
+  // One 32-key block at a time (scores, softmax, P V): keeps a single S
+  // block and its packed P live.
+  auto compute = [&](int step, const char* stage) {
     const int entry = ld_const(list, step >> 1);
     const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
     const bool partial = (entry & 3) == 1;
-    f32x16 s[2];
+    const char* kt = stage;
+    const char* vt = stage + kTileBytes;
+    const int* kids_lds = reinterpret_cast<const int*>(stage + 2 * kTileBytes);
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
-      s[kb2] = zero16();
-      const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kKvPitch + 8 * half];
+      f32x16 s = zero16();
+      const int krow = kb2 * 32 + (lane & 31);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s[kb2] = mfma32x32x16(ld_bf16x8(krow + ks * 16), qf[ks], s[kb2]);
-    }
-    if (partial) {
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2)
+      for (int ks = 0; ks < 4; ++ks) s = mfma32x32x16(tile_chunk(kt, krow, 2 * ks + half), qf[ks], s);
+      if (partial) {
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
-          const int4 kids = *reinterpret_cast<const int4*>(&lds.kid[buf][kk0]);
+          const int4 kids = *reinterpret_cast<const int4*>(&kids_lds[kk0]);
           const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const bool ok = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
-            s[kb2][g4 * 4 + i] = ok ? s[kb2][g4 * 4 + i] : kNegInf;
+            s[g4 * 4 + i] = ok ? s[g4 * 4 + i] : kNegInf;
           }
         }
-    }
-    float mx = kNegInf;
+      }
+      float mx = kNegInf;
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2)
+      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[r], s[r + 1]));
+      mx = halves_max(mx);
+      const bool grow = mx > m_used + tau;
+      if (__any(grow)) {
+        const float mnew = grow ? mx : m_used;
+        // a lane that has seen no valid key yet (m_used = -inf) has l = 0 and
+        // O = 0; give it alpha = 0 rather than exp2(-inf - -inf) = NaN
+        const float alpha = m_used == kNegInf ? 0.f : fast_exp2((m_used - mnew) * c);
+        m_used = mnew;
+        l *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[kb2][r], s[kb2][r + 1]));
-    mx = halves_max(mx);
-    const bool grow = mx > m_used + tau;
-    if (__any(grow)) {
-      const float mnew = grow ? mx : m_used;
-      // a lane that has seen no valid key yet (m_used = -inf) has l = 0 and
-      // O = 0; give it alpha = 0 rather than exp2(-inf - -inf) = NaN
-      const float alpha = m_used == kNegInf ? 0.f : fast_exp2((m_used - mnew) * c);
-      m_used = mnew;
-      l *= alpha;
+        for (int r = 0; r < 16; ++r) {
+          oacc[0][r] *= alpha;
+          oacc[1][r] *= alpha;
+        }
+      }
+      const float mc = m_used == kNegInf ? 0.f : m_used * c;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        oacc[0][r] *= alpha;
-        oacc[1][r] *= alpha;
+        s[r] = fast_exp2(fmaf(s[r], c, -mc));
+        l += s[r];
+      }
+      const bf16x8 p0 = pack8(s, 0), p1 = pack8(s, 8);
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const int col = db * 32 + tr_col;
+        oacc[db] = mfma32x32x16(tile_tr_operand(vt, kb2 * 32 + tr_row, col), p0, oacc[db]);
+        oacc[db] = mfma32x32x16(tile_tr_operand(vt, kb2 * 32 + 16 + tr_row, col), p1, oacc[db]);
       }
     }
-    const float mc = m_used == kNegInf ? 0.f : m_used * c;
-    bf16x8 pf[2][2];
-#pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[kb2][r] = fast_exp2(fmaf(s[kb2][r], c, -mc));
-      pf[kb2][0] = pack8(s[kb2], 0);
-      pf[kb2][1] = pack8(s[kb2], 8);
-#pragma unroll
-      for (int ks2 = 0; ks2 < 2; ++ks2) {
-        const u32x4 w = __builtin_bit_cast(u32x4, pf[kb2][ks2]);
-        l = add_bf16_pair(w[0], l);
-        l = add_bf16_pair(w[1], l);
-        l = add_bf16_pair(w[2], l);
-        l = add_bf16_pair(w[3], l);
-      }
-    }
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-        for (int ks2 = 0; ks2 < 2; ++ks2) {
-          const bf16x8 vt = tr_operand(lds.v[buf], kKvPitch, kb2 * 32 + ks2 * 16 + tr_row, db * 32 + tr_col);
-          oacc[db] = mfma32x32x16(vt, pf[kb2][ks2], oacc[db]);
-        }
   };
 
-  auto load = [&](int s, KvStepStage<T>& st) {
-    kvstep_load<T>(a.k, a.v, kid_row, kv_base, key_stride, a.S, step_kb(s), st);
-  };
-  KvStepStage<T> st0, st1;
+  constexpr int G = KvDma<W>::kPerStep;
   if (nsteps > 0) {
-    load(0, st0);
-    load(min(1, nsteps - 1), st1);
+    issue(0, stage0);
+    issue(1, stage1);
   }
-  if (nsteps > 0) kvstep_store<T>(st0, lds, 0);
-  __syncthreads();
-  // Prefetches are issued unconditionally (clamped to the last step, a
-  // harmless re-read) so the number of loads in flight is fixed and the
-  // wait before each LDS store covers only the older stage.
-  for (int step = 0; step < nsteps; step += 2) {
-    // even step: data in buffer 0; st1 holds step+1
-    load(min(step + 2, nsteps - 1), st0);
-    compute(step, 0);
-    if (step + 1 < nsteps) kvstep_store<T>(st1, lds, 1);
-    __syncthreads();
+  for (int step = 0; step < nsteps; step += 3) {
+    wait_vmcnt<G>();
+    barrier();
+    issue(step + 2, stage2);
+    compute(step, stage0);
     if (step + 1 >= nsteps) break;
-    // odd step: data in buffer 1; st0 holds step+2
-    load(min(step + 3, nsteps - 1), st1);
-    compute(step + 1, 1);
-    if (step + 2 < nsteps) kvstep_store<T>(st0, lds, 0);
-    __syncthreads();
+    wait_vmcnt<G>();
+    barrier();
+    issue(step + 3, stage0);
+    compute(step + 1, stage1);
+    if (step + 2 >= nsteps) break;
+    wait_vmcnt<G>();
+    barrier();
+    issue(step + 4, stage1);
+    compute(step + 2, stage2);
   }
+  wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 
   const bool qactive = qvalid && myqid != 0;
   const float lt = halves_sum(l);

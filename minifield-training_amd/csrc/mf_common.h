@@ -87,12 +87,6 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
-// Sum of the two bf16 halves of w plus acc (v_dot2c_f32_bf16 against 1.0).
-__device__ __forceinline__ float add_bf16_pair(uint32_t w, float acc) {
-  const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), ones, acc, false);
-}
-
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
