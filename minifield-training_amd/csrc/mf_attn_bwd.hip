@@ -20,6 +20,7 @@
 
 #include "mf_common.h"
 #include "mf_kvstep.h"
+#include "mf_lds.h"
 
 namespace mf {
 
@@ -672,16 +673,19 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16 dq: structure of the bf16 forward (one head per wave, 4*HPW waves,
-// K/V steps staged through LDS two steps ahead).  dQ^T += K^T dS^T takes its
-// K^T operand from the natural K tile through transposing LDS reads.
+// bf16 dq: the structure of the bf16 forward (one head per wave, 4*HPW
+// waves, K/V tiles DMA'd into a three-stage LDS ring two steps ahead).
+// dQ^T += K^T dS^T takes its K^T operand from the K tile through
+// transposing LDS reads.
 // ---------------------------------------------------------------------------
 template <int HPW>
-__global__ __launch_bounds__(256 * HPW) void bwd_dq_bf16_kernel(BwdArgs a) {
-  __shared__ KvStepLds lds;
-  constexpr int T = 256 * HPW;
+__global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2)))
+void bwd_dq_bf16_kernel(BwdArgs a) {
+  constexpr int W = 4 * HPW;
+  __shared__ __attribute__((aligned(16))) char stage0[kStageBytes], stage1[kStageBytes],
+      stage2[kStageBytes];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = uniform(threadIdx.x >> 6);
   const int half = lane >> 5;
   const int hr = blockIdx.x;
   const int b = uniform(hr / (a.Hkv * a.hchunks));
@@ -696,24 +700,20 @@ __global__ __launch_bounds__(256 * HPW) void bwd_dq_bf16_kernel(BwdArgs a) {
 
   bf16x8 qf[4], gf[4];
   {
-    const size_t row = (((size_t)b * a.T + qpos) * a.Hq + head) * kD + 8 * half;
+    const size_t row = (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
     const bf16* qs = reinterpret_cast<const bf16*>(a.q) + row;
     const bf16* gs = reinterpret_cast<const bf16*>(a.dout) + row;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      if (qvalid) {
-        qf[ks] = ld_bf16x8(qs + ks * 16);
-        gf[ks] = ld_bf16x8(gs + ks * 16);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[ks][e] = gf[ks][e] = (bf16)0.f;
-      }
+      qf[ks] = ld_bf16x8(qs + ks * 16);
+      gf[ks] = ld_bf16x8(gs + ks * 16);
     }
   }
-  const size_t li = ((size_t)b * a.Hq + head) * a.T + qpos;
-  const float lse2 = qactive ? a.lse[li] * kLog2e : kPosInf;
-  const float dlt = qvalid ? a.delta[li] : 0.f;
+  const size_t li = ((size_t)b * a.Hq + head) * a.T + min(qpos, a.T - 1);
+  const float lse_raw = a.lse[li], dlt_raw = a.delta[li];
   drain_memory();
+  const float lse2 = qactive ? lse_raw * kLog2e : kPosInf;
+  const float dlt = qactive ? dlt_raw : 0.f;
   f32x16 dqacc[2] = {zero16(), zero16()};
   const float c = a.scale_log2;
 
@@ -724,29 +724,36 @@ __global__ __launch_bounds__(256 * HPW) void bwd_dq_bf16_kernel(BwdArgs a) {
   const int tr_row = tr_row_of(lane);
   const int tr_col = tr_col_of(lane);
   const int* kid_row = a.kid + (size_t)b * a.tk_pad;
-  const size_t kv_base = ((size_t)b * a.S * a.Hkv + kvh) * kD;
-  const size_t key_stride = (size_t)a.Hkv * kD;
+  const size_t row_stride = (size_t)a.Hkv * kD * sizeof(bf16);
+  const char* kg = reinterpret_cast<const char*>(a.k) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
+  const char* vg = reinterpret_cast<const char*>(a.v) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
 
-  auto compute = [&](int step, int buf) {
+  auto issue = [&](int s, char* stage) {
+    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage);
+  };
+
+  auto compute = [&](int step, const char* stage) {
     const int entry = ld_const(list, step >> 1);
     const int kb = (entry >> 2) * kTile + (step & 1) * kKvStep;
     const bool partial = (entry & 3) == 1;
+    const char* kt = stage;
+    const char* vt = stage + kTileBytes;
+    const int* kids_lds = reinterpret_cast<const int*>(stage + 2 * kTileBytes);
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
       f32x16 s = zero16(), dp = zero16();
-      const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kKvPitch + 8 * half];
-      const bf16* vrow = &lds.v[buf][(kb2 * 32 + (lane & 31)) * kKvPitch + 8 * half];
+      const int krow = kb2 * 32 + (lane & 31);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        s = mfma32x32x16(ld_bf16x8(krow + ks * 16), qf[ks], s);
-        dp = mfma32x32x16(ld_bf16x8(vrow + ks * 16), gf[ks], dp);
+        s = mfma32x32x16(tile_chunk(kt, krow, 2 * ks + half), qf[ks], s);
+        dp = mfma32x32x16(tile_chunk(vt, krow, 2 * ks + half), gf[ks], dp);
       }
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         bool ok[4] = {true, true, true, true};
         if (partial) {
           const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
-          const int4 kids = *reinterpret_cast<const int4*>(&lds.kid[buf][kk0]);
+          const int4 kids = *reinterpret_cast<const int4*>(&kids_lds[kk0]);
           const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) ok[i] = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
@@ -762,33 +769,34 @@ __global__ __launch_bounds__(256 * HPW) void bwd_dq_bf16_kernel(BwdArgs a) {
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
         const int col = db * 32 + tr_col;
-        dqacc[db] = mfma32x32x16(tr_operand(lds.k[buf], kKvPitch, kb2 * 32 + tr_row, col), ds0, dqacc[db]);
-        dqacc[db] = mfma32x32x16(tr_operand(lds.k[buf], kKvPitch, kb2 * 32 + 16 + tr_row, col), ds1, dqacc[db]);
+        dqacc[db] = mfma32x32x16(tile_tr_operand(kt, kb2 * 32 + tr_row, col), ds0, dqacc[db]);
+        dqacc[db] = mfma32x32x16(tile_tr_operand(kt, kb2 * 32 + 16 + tr_row, col), ds1, dqacc[db]);
       }
     }
   };
 
-  auto load = [&](int s, KvStepStage<T>& st) {
-    kvstep_load<T>(a.k, a.v, kid_row, kv_base, key_stride, a.S, step_kb(s), st);
-  };
-  KvStepStage<T> st0, st1;
+  constexpr int G = KvDma<W>::kPerStep;
   if (nsteps > 0) {
-    load(0, st0);
-    load(min(1, nsteps - 1), st1);
+    issue(0, stage0);
+    issue(1, stage1);
   }
-  if (nsteps > 0) kvstep_store<T>(st0, lds, 0);
-  __syncthreads();
-  for (int step = 0; step < nsteps; step += 2) {
-    load(min(step + 2, nsteps - 1), st0);  // unconditional: see the forward
-    compute(step, 0);
-    if (step + 1 < nsteps) kvstep_store<T>(st1, lds, 1);
-    __syncthreads();
+  for (int step = 0; step < nsteps; step += 3) {
+    wait_vmcnt<G>();
+    barrier();
+    issue(step + 2, stage2);
+    compute(step, stage0);
     if (step + 1 >= nsteps) break;
-    load(min(step + 3, nsteps - 1), st1);
-    compute(step + 1, 1);
-    if (step + 2 < nsteps) kvstep_store<T>(st0, lds, 0);
-    __syncthreads();
+    wait_vmcnt<G>();
+    barrier();
+    issue(step + 3, stage0);
+    compute(step + 1, stage1);
+    if (step + 2 >= nsteps) break;
+    wait_vmcnt<G>();
+    barrier();
+    issue(step + 4, stage1);
+    compute(step + 2, stage2);
   }
+  wait_vmcnt<0>();
 
   if (!qvalid) return;
 #pragma unroll
@@ -809,34 +817,40 @@ __global__ __launch_bounds__(256 * HPW) void bwd_dq_bf16_kernel(BwdArgs a) {
 // Waves w and w+4 own the same 32 keys (K, V as B operands in registers) and
 // process different query heads of the GQA group (slot w/4 takes heads
 // slot, slot+HS, ...), so each query step stages Q and dO of HS heads; their
-// dK/dV are summed through LDS at the end.  dV^T += dO^T P and dK^T += Q^T dS
-// read their transposed operands from the natural Q / dO tiles.
+// dK/dV are summed through LDS at the end.  Q, dO, lse, D and the query ids
+// are DMA'd into a three-stage LDS ring two steps ahead; dV^T += dO^T P and
+// dK^T += Q^T dS read their transposed operands from the Q / dO tiles.
 // ---------------------------------------------------------------------------
 template <int HS>
-struct DkdvLds {
-  bf16 q[2][HS][kKvStep * kKvPitch];
-  bf16 g[2][HS][kKvStep * kKvPitch];
-  float lse2[2][HS][kKvStep];
-  float dlt[2][HS][kKvStep];
-  int qid[2][kKvStep];
+struct QDma {
+  static constexpr int W = 4 * HS;
+  static constexpr int kTiles = 2 * HS;                      // Q, dO per slot
+  static constexpr int kGroupsPerWave = kTiles * 8 / W;      // 8-row groups
+  static constexpr int kWordArrays = 2 * HS + 1;             // lse, D per slot; ids
+  static_assert(kWordArrays <= W, "one word array per wave");
+  // Waves below kWordArrays issue one more DMA per step than the others; the
+  // step wait uses the smaller count, which for them also covers the oldest
+  // DMA of the stage issued one step earlier.
+  static constexpr int kPerStep = kGroupsPerWave;
+  // stage layout: tiles [slot][Q, dO], then lse[slot][64], D[slot][64], ids[64]
+  static constexpr int kLseOff = kTiles * kTileBytes;
+  static constexpr int kDltOff = kLseOff + HS * 256;
+  static constexpr int kIdOff = kDltOff + HS * 256;
+  static constexpr int kStageBytes = kIdOff + 256;
 };
 
 template <int HS>
-struct DkdvStage {
-  u32x4 r[4];
-  float lse2, dlt;
-  int qid;
-};
-
-template <int HS>
-__global__ __launch_bounds__(256 * HS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
-  __shared__ DkdvLds<HS> lds;
-  constexpr int T = 256 * HS;
+__global__ __launch_bounds__(256 * HS) __attribute__((amdgpu_waves_per_eu(2)))
+void bwd_dkdv_bf16_kernel(BwdArgs a) {
+  using Q = QDma<HS>;
+  constexpr int W = Q::W;
+  __shared__ __attribute__((aligned(16))) char stage0[Q::kStageBytes], stage1[Q::kStageBytes],
+      stage2[Q::kStageBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = uniform(tid >> 6);
   const int half = lane >> 5;
-  const int slot = wave >> 2;
+  const int slot = HS == 1 ? 0 : wave >> 2;
   const int b = uniform(blockIdx.x / a.Hkv);
   const int kvh = uniform(blockIdx.x % a.Hkv);
   const int kt = uniform(blockIdx.y);
@@ -846,18 +860,13 @@ __global__ __launch_bounds__(256 * HS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
 
   bf16x8 kf[4], vf[4];
   {
-    const size_t row = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD + 8 * half;
+    const size_t row = (((size_t)b * a.S + min(kpos, a.S - 1)) * a.Hkv + kvh) * kD + 8 * half;
     const bf16* ks = reinterpret_cast<const bf16*>(a.k) + row;
     const bf16* vs = reinterpret_cast<const bf16*>(a.v) + row;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (kvalid) {
-        kf[i] = ld_bf16x8(ks + i * 16);
-        vf[i] = ld_bf16x8(vs + i * 16);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kf[i][e] = vf[i][e] = (bf16)0.f;
-      }
+      kf[i] = ld_bf16x8(ks + i * 16);
+      vf[i] = ld_bf16x8(vs + i * 16);
     }
   }
   drain_memory();
@@ -869,83 +878,79 @@ __global__ __launch_bounds__(256 * HS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
   const int per_tile = hps * 2;    // (head, 64-query half) iterations per query tile
   const int niters = count * per_tile;
   const float c = a.scale_log2;
-  const int tr_row = tr_row_of(lane);
-  const int tr_col = tr_col_of(lane);
+  const size_t qrow_stride = (size_t)a.Hq * kD * sizeof(bf16);
 
-  auto iter = [&](int it, int& qb, int& hj, int& cls) {
+  // DMA of iteration `it` (query rows qb .. qb+63 of HS heads) into a stage.
+  auto issue = [&](int it, char* stage) {
+    it = min(it, niters - 1);
     const int entry = ld_const(list, it / per_tile);
     const int rem = it % per_tile;
-    hj = rem >> 1;
-    qb = (entry >> 2) * kTile + (rem & 1) * kKvStep;
-    cls = entry & 3;
-  };
-  auto load = [&](int it, DkdvStage<HS>& st) {
-    int qb, hj, cls;
-    iter(it, qb, hj, cls);
+    const int hj = rem >> 1;
+    const int qb = (entry >> 2) * kTile + (rem & 1) * kKvStep;
+    // the word arrays first, so the short step wait covers them
+    if (wave < Q::kWordArrays) {
+      const int qq = min(qb + lane, a.T - 1);
+      // rows past T re-read row T-1 (finite values); their ids are 0, so
+      // every pair they form is masked or belongs to a zeroed inactive key
+      const int s = min(wave >> 1, HS - 1);
+      const size_t li = ((size_t)b * a.Hq + kvh * a.G + s + HS * hj) * a.T + qq;
+      const void* src = wave == 2 * HS ? (const void*)(a.qid + (size_t)b * a.tq_pad + qb + lane)
+                        : (wave & 1) ? (const void*)(a.delta + li)
+                                     : (const void*)(a.lse + li);
+      char* dst = wave == 2 * HS ? stage + Q::kIdOff
+                  : (wave & 1)   ? stage + Q::kDltOff + s * 256
+                                 : stage + Q::kLseOff + s * 256;
+      dma_word64(src, dst);
+    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + T * i;           // (slot, tensor, row, chunk)
-      const int s = u >> 10, tensor = (u >> 9) & 1, row = (u & 511) >> 3, ch = u & 7;
+    for (int j = 0; j < Q::kGroupsPerWave; ++j) {
+      const int g = wave + W * j;              // global 8-row group index
+      const int tile = g >> 3, r0 = 8 * (g & 7);
+      const int s = tile >> 1;                 // head slot of this tile
       const int h = kvh * a.G + s + HS * hj;
-      // rows past the end re-read the last row; their P is 0 (lse = +inf)
-      const int qq = min(qb + row, a.T - 1);
-      const bf16* src = reinterpret_cast<const bf16*>(tensor ? a.dout : a.q);
-      st.r[i] = ld_u32x4(src + (((size_t)b * a.T + qq) * a.Hq + h) * kD + ch * 8);
-    }
-    {
-      // every thread loads (clamped, in bounds) so no load sits in a branch
-      const int s = (tid >> 6) % HS, qq = qb + (tid & 63);
-      const int h = kvh * a.G + s + HS * hj;
-      const int id = a.qid[(size_t)b * a.tq_pad + qq];
-      const bool act = qq < a.T && id != 0;
-      const size_t li = ((size_t)b * a.Hq + h) * a.T + min(qq, a.T - 1);
-      const float lse = a.lse[li], dl = a.delta[li];
-      st.qid = id;
-      st.lse2 = act ? lse * kLog2e : kPosInf;
-      st.dlt = act ? dl : 0.f;
-    }
-  };
-  auto store = [&](const DkdvStage<HS>& st, int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + T * i;
-      const int s = u >> 10, tensor = (u >> 9) & 1, row = (u & 511) >> 3, ch = u & 7;
-      st_u32x4((tensor ? lds.g[buf][s] : lds.q[buf][s]) + row * kKvPitch + ch * 8, st.r[i]);
-    }
-    if (tid < kKvStep * HS) {
-      const int s = tid >> 6, r = tid & 63;
-      lds.lse2[buf][s][r] = st.lse2;
-      lds.dlt[buf][s][r] = st.dlt;
-      if (s == 0) lds.qid[buf][r] = st.qid;
+      const char* base = reinterpret_cast<const char*>((tile & 1) ? a.dout : a.q) +
+                         ((size_t)b * a.T * a.Hq + h) * kD * sizeof(bf16);
+      dma_rows8(base, qrow_stride, qb, r0, a.T - 1, stage + tile * kTileBytes);
     }
   };
 
-  auto compute = [&](int it, int buf) {
-    int qb, hj, cls;
-    iter(it, qb, hj, cls);
-    const bool partial = cls == 1;
-    const bf16* qt = lds.q[buf][slot];
-    const bf16* gt = lds.g[buf][slot];
-#pragma unroll 1
+  auto compute = [&](int it, const char* stage) {
+    const int entry = ld_const(list, it / per_tile);
+    const int rem = it % per_tile;
+    const int qb = (entry >> 2) * kTile + (rem & 1) * kKvStep;
+    const bool partial = (entry & 3) == 1;
+    // a select between constant offsets (not slot * size) keeps the tile
+    // addresses analysable, so the compiler can tell these reads from the
+    // DMAs in flight to the other stages and inserts no wait for them
+    const char* qt = slot ? stage + 2 * kTileBytes : stage;
+    const char* gt = slot ? stage + 3 * kTileBytes : stage + kTileBytes;
+    const float* lse_l = reinterpret_cast<const float*>(stage + Q::kLseOff + slot * 256);
+    const float* dlt_l = reinterpret_cast<const float*>(stage + Q::kDltOff + slot * 256);
+    const int* qid_l = reinterpret_cast<const int*>(stage + Q::kIdOff);
+    const int tr_row = tr_row_of(lane);
+    const int tr_col = tr_col_of(lane);
+    // Fully unrolled: an inner loop header here would make the compiler's
+    // wait insertion give up tracking which LDS stage each DMA in flight
+    // targets and wait for all of them (vmcnt(0)).
+#pragma unroll
     for (int qb2 = 0; qb2 < 2; ++qb2) {
       f32x16 s = zero16(), dp = zero16();
-      const bf16* qrow = qt + (qb2 * 32 + (lane & 31)) * kKvPitch + 8 * half;
-      const bf16* grow = gt + (qb2 * 32 + (lane & 31)) * kKvPitch + 8 * half;
+      const int qrow = qb2 * 32 + (lane & 31);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        s = mfma32x32x16(ld_bf16x8(qrow + ks * 16), kf[ks], s);
-        dp = mfma32x32x16(ld_bf16x8(grow + ks * 16), vf[ks], dp);
+        s = mfma32x32x16(tile_chunk(qt, qrow, 2 * ks + half), kf[ks], s);
+        dp = mfma32x32x16(tile_chunk(gt, qrow, 2 * ks + half), vf[ks], dp);
       }
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int qq0 = qb2 * 32 + 8 * g4 + 4 * half;
-        const float4 l4 = *reinterpret_cast<const float4*>(&lds.lse2[buf][slot][qq0]);
-        const float4 d4 = *reinterpret_cast<const float4*>(&lds.dlt[buf][slot][qq0]);
+        const float4 l4 = *reinterpret_cast<const float4*>(&lse_l[qq0]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&dlt_l[qq0]);
         const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
         const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
         bool ok[4] = {true, true, true, true};
         if (partial) {
-          const int4 ids = *reinterpret_cast<const int4*>(&lds.qid[buf][qq0]);
+          const int4 ids = *reinterpret_cast<const int4*>(&qid_l[qq0]);
           const int iv[4] = {ids.x, ids.y, ids.z, ids.w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) ok[i] = iv[i] == mykid && (!a.causal || kpos <= qb + qq0 + i);
@@ -953,7 +958,7 @@ __global__ __launch_bounds__(256 * HS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = g4 * 4 + i;
-          const float p = ok[i] ? fast_exp2(fmaf(s[r], c, -lv[i])) : 0.f;
+          const float p = ok[i] ? fast_exp2(fmaf(s[r], c, -lv[i] * kLog2e)) : 0.f;
           s[r] = p;
           dp[r] = p * (dp[r] - dv4[i]);
         }
@@ -964,44 +969,53 @@ __global__ __launch_bounds__(256 * HS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
       for (int db = 0; db < 2; ++db) {
         const int col = db * 32 + tr_col;
         const int r0 = qb2 * 32 + tr_row;
-        dvacc[db] = mfma32x32x16(tr_operand(gt, kKvPitch, r0, col), pf0, dvacc[db]);
-        dvacc[db] = mfma32x32x16(tr_operand(gt, kKvPitch, r0 + 16, col), pf1, dvacc[db]);
-        dkacc[db] = mfma32x32x16(tr_operand(qt, kKvPitch, r0, col), sf0, dkacc[db]);
-        dkacc[db] = mfma32x32x16(tr_operand(qt, kKvPitch, r0 + 16, col), sf1, dkacc[db]);
+        dvacc[db] = mfma32x32x16(tile_tr_operand(gt, r0, col), pf0, dvacc[db]);
+        dvacc[db] = mfma32x32x16(tile_tr_operand(gt, r0 + 16, col), pf1, dvacc[db]);
+        dkacc[db] = mfma32x32x16(tile_tr_operand(qt, r0, col), sf0, dkacc[db]);
+        dkacc[db] = mfma32x32x16(tile_tr_operand(qt, r0 + 16, col), sf1, dkacc[db]);
       }
     }
   };
 
-  DkdvStage<HS> st0, st1;
+  constexpr int G = Q::kPerStep;
   if (niters > 0) {
-    load(0, st0);
-    load(min(1, niters - 1), st1);
-    store(st0, 0);
+    issue(0, stage0);
+    issue(1, stage1);
   }
-  __syncthreads();
-  for (int it = 0; it < niters; it += 2) {
-    load(min(it + 2, niters - 1), st0);  // unconditional prefetch (see the forward)
-    compute(it, 0);
-    if (it + 1 < niters) store(st1, 1);
-    __syncthreads();
-    if (it + 1 >= niters) break;
-    load(min(it + 3, niters - 1), st1);
-    compute(it + 1, 1);
-    if (it + 2 < niters) store(st0, 0);
-    __syncthreads();
+  // The loop runs whole groups of three steps and skips the compute of the
+  // (at most two) steps past the end: a mid-group exit would give the
+  // accumulators three different exit paths, which the register allocator
+  // resolves with 64-register copies.
+  for (int it = 0; it < niters; it += 3) {
+    wait_vmcnt<G>();
+    barrier();
+    issue(it + 2, stage2);
+    compute(it, stage0);
+    wait_vmcnt<G>();
+    barrier();
+    issue(it + 3, stage0);
+    if (it + 1 < niters) compute(it + 1, stage1);
+    wait_vmcnt<G>();
+    barrier();
+    issue(it + 4, stage1);
+    if (it + 2 < niters) compute(it + 2, stage2);
   }
+  wait_vmcnt<0>();
 
   if constexpr (HS == 2) {
-    // slot 1 hands its partial dK/dV to slot 0 through LDS (staging is idle)
-    float* red = reinterpret_cast<float*>(&lds);
-    float* mine = red + ((wave & 3) * 64 + lane) * 64;
+    // slot 1 hands its partial dK (through stage0) and dV (through stage1)
+    // to slot 0; the ring is idle once every wave has passed the barrier
+    static_assert(4 * 64 * 32 * sizeof(float) <= Q::kStageBytes, "reduction buffer");
+    barrier();
+    float* kred = reinterpret_cast<float*>(stage0) + ((wave & 3) * 64 + lane) * 32;
+    float* vred = reinterpret_cast<float*>(stage1) + ((wave & 3) * 64 + lane) * 32;
     if (slot == 1) {
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          mine[db * 16 + r] = dkacc[db][r];
-          mine[32 + db * 16 + r] = dvacc[db][r];
+          kred[db * 16 + r] = dkacc[db][r];
+          vred[db * 16 + r] = dvacc[db][r];
         }
     }
     __syncthreads();
@@ -1010,8 +1024,8 @@ __global__ __launch_bounds__(256 * HS) void bwd_dkdv_bf16_kernel(BwdArgs a) {
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        dkacc[db][r] += mine[db * 16 + r];
-        dvacc[db][r] += mine[32 + db * 16 + r];
+        dkacc[db][r] += kred[db * 16 + r];
+        dvacc[db][r] += vred[db * 16 + r];
       }
   }
   if (!kvalid) return;
@@ -1095,6 +1109,8 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   if (phases & 4) {
     if (f32)
       hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);
+    else if (a.G % 2 == 0)
+      hipLaunchKernelGGL((bwd_dkdv_bf16_kernel<2>), kgrid, dim3(512), 0, stream, a);
     else
       hipLaunchKernelGGL((bwd_dkdv_bf16_kernel<1>), kgrid, dim3(256), 0, stream, a);
   }

@@ -380,29 +380,6 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
 // log2 units, so P <= 2^8 and the final division by the row sum is
 // unchanged.  Row sums are fp32 adds (v_dot2 would occupy the matrix pipe).
 // ---------------------------------------------------------------------------
-constexpr int kStageBytes = 2 * kTileBytes + 256;  // K tile, V tile, 64 key ids
-
-template <int W>
-struct KvDma {
-  static constexpr int kGroups = 8 / W;            // 8-row groups per tile per wave
-  static constexpr int kIds = 64 / W;              // key ids per wave
-  static constexpr int kPerStep = 2 * kGroups + 1; // DMA instructions per wave per step
-};
-
-// DMA of keys kb .. kb+63 (K rows, V rows, canonical ids) into one stage.
-template <int W>
-__device__ __forceinline__ void kv_dma(const char* kg, const char* vg, size_t row_stride, int S,
-                                       const int* kid_row, int kb, int wave, char* stage) {
-#pragma unroll
-  for (int j = 0; j < KvDma<W>::kGroups; ++j) {
-    const int r0 = 8 * (wave + W * j);
-    dma_rows8(kg, row_stride, kb, r0, S - 1, stage);
-    dma_rows8(vg, row_stride, kb, r0, S - 1, stage + kTileBytes);
-  }
-  constexpr int E = KvDma<W>::kIds;
-  dma_words(kid_row + kb + E * wave, stage + 2 * kTileBytes + 4 * E * wave, E);
-}
-
 template <int HPW>
 __global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2 * HPW)))
 void attn_fwd_bf16_kernel(FwdArgs a) {

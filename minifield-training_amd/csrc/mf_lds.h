@@ -51,6 +51,13 @@ __device__ __forceinline__ void dma_words(const void* src, void* dst, int count)
                                      0, 0);
 }
 
+// One 4-byte word per lane, all 64 lanes: lane L's word (read from its own
+// address `src`) lands at dst + 4 L.  Unconditional, so it adds no
+// divergent branch to the staging code.
+__device__ __forceinline__ void dma_word64(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(reinterpret_cast<const int*>(src), (lds_void_ptr)dst, 4, 0, 0);
+}
+
 // 16-byte operand: chunk c of row r.
 __device__ __forceinline__ bf16x8 tile_chunk(const char* tile, int r, int c) {
   return *reinterpret_cast<const bf16x8*>(tile + chunk_off(r, c));
@@ -75,5 +82,29 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 __device__ __forceinline__ void barrier() { __builtin_amdgcn_s_barrier(); }
+
+// One stage of the key-side ring: K tile, V tile and the 64 canonical key ids.
+constexpr int kStageBytes = 2 * kTileBytes + 256;  // K tile, V tile, 64 key ids
+
+template <int W>
+struct KvDma {
+  static constexpr int kGroups = 8 / W;            // 8-row groups per tile per wave
+  static constexpr int kIds = 64 / W;              // key ids per wave
+  static constexpr int kPerStep = 2 * kGroups + 1; // DMA instructions per wave per step
+};
+
+// DMA of keys kb .. kb+63 (K rows, V rows, canonical ids) into one stage.
+template <int W>
+__device__ __forceinline__ void kv_dma(const char* kg, const char* vg, size_t row_stride, int S,
+                                       const int* kid_row, int kb, int wave, char* stage) {
+#pragma unroll
+  for (int j = 0; j < KvDma<W>::kGroups; ++j) {
+    const int r0 = 8 * (wave + W * j);
+    dma_rows8(kg, row_stride, kb, r0, S - 1, stage);
+    dma_rows8(vg, row_stride, kb, r0, S - 1, stage + kTileBytes);
+  }
+  constexpr int E = KvDma<W>::kIds;
+  dma_words(kid_row + kb + E * wave, stage + 2 * kTileBytes + 4 * E * wave, E);
+}
 
 }  // namespace mf
