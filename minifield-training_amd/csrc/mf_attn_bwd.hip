@@ -768,9 +768,10 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
       const bf16x8 ds0 = pack8(s, 0), ds1 = pack8(s, 8);
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
-        const int col = db * 32 + tr_col;
-        dqacc[db] = mfma32x32x16(tile_tr_operand(kt, kb2 * 32 + tr_row, col), ds0, dqacc[db]);
-        dqacc[db] = mfma32x32x16(tile_tr_operand(kt, kb2 * 32 + 16 + tr_row, col), ds1, dqacc[db]);
+        const bf16x8 k0 = tile_tr_operand(kt, kb2 * 32 + tr_row, db * 32 + tr_col);
+        const bf16x8 k1 = tile_tr_operand(kt, kb2 * 32 + 16 + tr_row, db * 32 + tr_col);
+        dqacc[db] = mfma32x32x16(k0, ds0, dqacc[db]);
+        dqacc[db] = mfma32x32x16(k1, ds1, dqacc[db]);
       }
     }
   };
@@ -780,21 +781,22 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     issue(0, stage0);
     issue(1, stage1);
   }
+  // Whole groups of three steps; the compute of steps past the end is
+  // skipped rather than leaving the loop mid-group (a mid-group exit gives the
+  // accumulators three exit paths, resolved with register copies).
   for (int step = 0; step < nsteps; step += 3) {
     wait_vmcnt<G>();
     barrier();
     issue(step + 2, stage2);
     compute(step, stage0);
-    if (step + 1 >= nsteps) break;
     wait_vmcnt<G>();
     barrier();
     issue(step + 3, stage0);
-    compute(step + 1, stage1);
-    if (step + 2 >= nsteps) break;
+    if (step + 1 < nsteps) compute(step + 1, stage1);
     wait_vmcnt<G>();
     barrier();
     issue(step + 4, stage1);
-    compute(step + 2, stage2);
+    if (step + 2 < nsteps) compute(step + 2, stage2);
   }
   wait_vmcnt<0>();
 
@@ -965,14 +967,17 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
       }
       const bf16x8 pf0 = pack8(s, 0), pf1 = pack8(s, 8);
       const bf16x8 sf0 = pack8(dp, 0), sf1 = pack8(dp, 8);
+      const int r0 = qb2 * 32 + tr_row;
 #pragma unroll
       for (int db = 0; db < 2; ++db) {
-        const int col = db * 32 + tr_col;
-        const int r0 = qb2 * 32 + tr_row;
-        dvacc[db] = mfma32x32x16(tile_tr_operand(gt, r0, col), pf0, dvacc[db]);
-        dvacc[db] = mfma32x32x16(tile_tr_operand(gt, r0 + 16, col), pf1, dvacc[db]);
-        dkacc[db] = mfma32x32x16(tile_tr_operand(qt, r0, col), sf0, dkacc[db]);
-        dkacc[db] = mfma32x32x16(tile_tr_operand(qt, r0 + 16, col), sf1, dkacc[db]);
+        const bf16x8 g0 = tile_tr_operand(gt, r0, db * 32 + tr_col);
+        const bf16x8 g1 = tile_tr_operand(gt, r0 + 16, db * 32 + tr_col);
+        dvacc[db] = mfma32x32x16(g0, pf0, dvacc[db]);
+        dvacc[db] = mfma32x32x16(g1, pf1, dvacc[db]);
+        const bf16x8 q0 = tile_tr_operand(qt, r0, db * 32 + tr_col);
+        const bf16x8 q1 = tile_tr_operand(qt, r0 + 16, db * 32 + tr_col);
+        dkacc[db] = mfma32x32x16(q0, sf0, dkacc[db]);
+        dkacc[db] = mfma32x32x16(q1, sf1, dkacc[db]);
       }
     }
   };

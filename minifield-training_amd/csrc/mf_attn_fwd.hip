@@ -430,8 +430,78 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage);
   };
 
-  // One 32-key block at a time (scores, softmax, P V): keeps a single S
-  // block and its packed P live.
+  // Sub-block classification inside PARTIAL tiles.  A wave's 32 queries
+  // against one 32-key block are skipped when no pair can be valid, run
+  // without masks when every pair is valid, and masked otherwise (ids only,
+  // causal only, or both).  When the wave's query ids are not all equal
+  // every block of a PARTIAL tile is masked.
+  const int q0 = qt * kTile + (wave & 3) * 32;
+  const int u = uniform(myqid);
+  const bool quni = __all(myqid == u);
+
+  auto scores = [&](const char* kt, int kb2) {
+    f32x16 s = zero16();
+    const int krow = kb2 * 32 + (lane & 31);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) s = mfma32x32x16(tile_chunk(kt, krow, 2 * ks + half), qf[ks], s);
+    return s;
+  };
+
+  // masks (ids and/or causal), online softmax, O += P V for one block
+  auto softmax_pv = [&](f32x16& s, const char* vt, const int* kids_lds, int kb, int kb2,
+                        bool mask_ids, bool diag) {
+    if (mask_ids) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
+        const int4 kids = *reinterpret_cast<const int4*>(&kids_lds[kk0]);
+        const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[g4 * 4 + i] = kv[i] == myqid ? s[g4 * 4 + i] : kNegInf;
+      }
+    }
+    if (diag) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        s[r] = kb + kb2 * 32 + acc_row(r, lane) <= qpos ? s[r] : kNegInf;
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[r], s[r + 1]));
+    mx = halves_max(mx);
+    const bool grow = mx > m_used + tau;
+    if (__any(grow)) {
+      const float mnew = grow ? mx : m_used;
+      // a lane that has seen no valid key yet (m_used = -inf) has l = 0 and
+      // O = 0; give it alpha = 0 rather than exp2(-inf - -inf) = NaN
+      const float alpha = m_used == kNegInf ? 0.f : fast_exp2((m_used - mnew) * c);
+      m_used = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        oacc[0][r] *= alpha;
+        oacc[1][r] *= alpha;
+      }
+    }
+    const float mc = m_used == kNegInf ? 0.f : m_used * c;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = fast_exp2(fmaf(s[r], c, -mc));
+      l += s[r];
+    }
+    const bf16x8 p0 = pack8(s, 0), p1 = pack8(s, 8);
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const bf16x8 v0 = tile_tr_operand(vt, kb2 * 32 + tr_row, db * 32 + tr_col);
+      const bf16x8 v1 = tile_tr_operand(vt, kb2 * 32 + 16 + tr_row, db * 32 + tr_col);
+      oacc[db] = mfma32x32x16(v0, p0, oacc[db]);
+      oacc[db] = mfma32x32x16(v1, p1, oacc[db]);
+    }
+  };
+
+  // One step = two 32-key blocks.  Both score blocks are issued before the
+  // softmax of the first, so the second block's MFMAs run under that VALU
+  // work (and the first block's P V under the second block's softmax).
   auto compute = [&](int step, const char* stage) {
     const int entry = ld_const(list, step >> 1);
     const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
@@ -439,57 +509,28 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     const char* kt = stage;
     const char* vt = stage + kTileBytes;
     const int* kids_lds = reinterpret_cast<const int*>(stage + 2 * kTileBytes);
+    bool run[2] = {true, true}, mask_ids[2] = {false, false}, diag[2] = {false, false};
+    if (partial) {
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2) {
-      f32x16 s = zero16();
-      const int krow = kb2 * 32 + (lane & 31);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) s = mfma32x32x16(tile_chunk(kt, krow, 2 * ks + half), qf[ks], s);
-      if (partial) {
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
-          const int4 kids = *reinterpret_cast<const int4*>(&kids_lds[kk0]);
-          const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool ok = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
-            s[g4 * 4 + i] = ok ? s[g4 * 4 + i] : kNegInf;
-          }
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+        const int k0 = kb + kb2 * 32;
+        const bool above = a.causal && k0 > q0 + 31;
+        diag[kb2] = a.causal && k0 + 31 > q0;
+        if (quni) {
+          const uint64_t m = __ballot(kids_lds[kb2 * 32 + (lane & 31)] == u);
+          run[kb2] = !above && u != 0 && m != 0;
+          mask_ids[kb2] = m != ~0ull;
+        } else {
+          run[kb2] = !above;
+          mask_ids[kb2] = true;
         }
-      }
-      float mx = kNegInf;
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[r], s[r + 1]));
-      mx = halves_max(mx);
-      const bool grow = mx > m_used + tau;
-      if (__any(grow)) {
-        const float mnew = grow ? mx : m_used;
-        // a lane that has seen no valid key yet (m_used = -inf) has l = 0 and
-        // O = 0; give it alpha = 0 rather than exp2(-inf - -inf) = NaN
-        const float alpha = m_used == kNegInf ? 0.f : fast_exp2((m_used - mnew) * c);
-        m_used = mnew;
-        l *= alpha;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          oacc[0][r] *= alpha;
-          oacc[1][r] *= alpha;
-        }
-      }
-      const float mc = m_used == kNegInf ? 0.f : m_used * c;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s[r] = fast_exp2(fmaf(s[r], c, -mc));
-        l += s[r];
-      }
-      const bf16x8 p0 = pack8(s, 0), p1 = pack8(s, 8);
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const int col = db * 32 + tr_col;
-        oacc[db] = mfma32x32x16(tile_tr_operand(vt, kb2 * 32 + tr_row, col), p0, oacc[db]);
-        oacc[db] = mfma32x32x16(tile_tr_operand(vt, kb2 * 32 + 16 + tr_row, col), p1, oacc[db]);
       }
     }
+    f32x16 s0, s1;
+    if (run[0]) s0 = scores(kt, 0);
+    if (run[1]) s1 = scores(kt, 1);
+    if (run[0]) softmax_pv(s0, vt, kids_lds, kb, 0, mask_ids[0], diag[0]);
+    if (run[1]) softmax_pv(s1, vt, kids_lds, kb, 1, mask_ids[1], diag[1]);
   };
 
   constexpr int G = KvDma<W>::kPerStep;
@@ -497,21 +538,22 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     issue(0, stage0);
     issue(1, stage1);
   }
+  // Whole groups of three steps; the compute of steps past the end is
+  // skipped rather than leaving the loop mid-group (a mid-group exit gives the
+  // accumulators three exit paths, resolved with register copies).
   for (int step = 0; step < nsteps; step += 3) {
     wait_vmcnt<G>();
     barrier();
     issue(step + 2, stage2);
     compute(step, stage0);
-    if (step + 1 >= nsteps) break;
     wait_vmcnt<G>();
     barrier();
     issue(step + 3, stage0);
-    compute(step + 1, stage1);
-    if (step + 2 >= nsteps) break;
+    if (step + 1 < nsteps) compute(step + 1, stage1);
     wait_vmcnt<G>();
     barrier();
     issue(step + 4, stage1);
-    compute(step + 2, stage2);
+    if (step + 2 < nsteps) compute(step + 2, stage2);
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 

@@ -11,10 +11,20 @@
 // moves 8 rows per instruction; the swizzle is applied on the source side by
 // choosing which global chunk each lane fetches.
 //
-// Synchronisation is explicit: the staging loop waits on this wave's own DMAs
-// with vmcnt(N) and then crosses a raw s_barrier.  __syncthreads() would add a
-// release fence that waits for every DMA in flight, including the ones
-// prefetching later stages.
+// The DMAs, the vmcnt waits and the barriers are issued as inline asm with
+// "memory" clobbers, and synchronisation is explicit: a staging loop waits on
+// its own DMAs with vmcnt(N) and then crosses s_barrier.  The compiler is not
+// told about the DMAs on purpose.  Its wait insertion tracks which LDS object
+// a DMA in flight writes only as far as its alias analysis reaches, and when
+// that fails for a later LDS read (which happens for reads in conditionally
+// executed blocks) it waits for every DMA in flight, including the ones that
+// prefetch later stages, so the ring no longer overlaps copies with compute.
+// The asm statements are also compiler memory barriers, so no LDS access is
+// moved across a DMA issue, a wait or a barrier.
+//
+// The DMA asm writes M0 (the LDS destination).  No other instruction in the
+// kernels that include this header uses M0, so nothing the compiler keeps in
+// M0 is lost.
 #pragma once
 
 #include "mf_common.h"
@@ -30,32 +40,39 @@ __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 
 
 __device__ __forceinline__ int chunk_off(int r, int c) { return r * kRowBytes + ((c ^ swz(r)) << 4); }
 
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(uintptr_t)p;  // low 32 bits of a generic LDS address
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is reserved; see the header comment
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Tile rows r0 .. r0+7 = global rows first + r0 .. first + r0 + 7 (global
 // row 0 at g_base, rows row_stride bytes apart; rows past `last` re-read row
-// `last`, so every access stays inside the tensor) into the LDS tile.
+// `last`, so every access stays inside the tensor) into the LDS tile.  The
+// tile address and r0 must be wave-uniform.
 __device__ __forceinline__ void dma_rows8(const char* g_base, size_t row_stride, int first, int r0,
                                           int last, char* tile) {
   const int lane = __lane_id();
   const int r = r0 + (lane >> 3);
   const int c = (lane & 7) ^ swz(r);
   const char* src = g_base + (size_t)min(first + r, last) * row_stride + c * 16;
-  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)(tile + r0 * kRowBytes), 16, 0, 0);
-}
-
-// `count` consecutive 4-byte words (count <= 64), lanes >= count idle:
-// dst[i] = src[i].  Used for the per-row ids and softmax statistics.
-__device__ __forceinline__ void dma_words(const void* src, void* dst, int count) {
-  const int lane = __lane_id();
-  if (lane < count)
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const int*>(src) + lane, (lds_void_ptr)dst, 4,
-                                     0, 0);
+  dma16(src, uniform((int)lds_offset(tile + r0 * kRowBytes)));
 }
 
 // One 4-byte word per lane, all 64 lanes: lane L's word (read from its own
-// address `src`) lands at dst + 4 L.  Unconditional, so it adds no
-// divergent branch to the staging code.
+// address `src`) lands at dst + 4 L (dst wave-uniform).
 __device__ __forceinline__ void dma_word64(const void* src, void* dst) {
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const int*>(src), (lds_void_ptr)dst, 4, 0, 0);
+  dma4(src, uniform((int)lds_offset(dst)));
 }
 
 // 16-byte operand: chunk c of row r.
@@ -68,20 +85,21 @@ __device__ __forceinline__ bf16x8 tile_chunk(const char* tile, int r, int c) {
 // column col (a multiple of 4), read with ds_read_b64_tr_b16.
 __device__ __forceinline__ bf16x8 tile_tr_operand(const char* tile, int row, int col) {
   const int c = col >> 3, within = (col & 7) * 2;
-  const u32x2 lo = lds_read_tr16(tile + row * kRowBytes + ((c ^ swz(row)) << 4) + within);
-  const int row2 = row + 8;
-  const u32x2 hi = lds_read_tr16(tile + row2 * kRowBytes + ((c ^ swz(row2)) << 4) + within);
+  // swz(row + 8) == swz(row): the second read is 8 rows (1 KiB) further on
+  const char* p = tile + row * kRowBytes + ((c ^ swz(row)) << 4) + within;
+  const u32x2 lo = lds_read_tr16(p);
+  const u32x2 hi = lds_read_tr16(p + 8 * kRowBytes);
   const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
   return __builtin_bit_cast(bf16x8, w);
 }
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate out of range");
-  __builtin_amdgcn_s_waitcnt(0xF70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate out of range");
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
-__device__ __forceinline__ void barrier() { __builtin_amdgcn_s_barrier(); }
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // One stage of the key-side ring: K tile, V tile and the 64 canonical key ids.
 constexpr int kStageBytes = 2 * kTileBytes + 256;  // K tile, V tile, 64 key ids
@@ -89,22 +107,24 @@ constexpr int kStageBytes = 2 * kTileBytes + 256;  // K tile, V tile, 64 key ids
 template <int W>
 struct KvDma {
   static constexpr int kGroups = 8 / W;            // 8-row groups per tile per wave
-  static constexpr int kIds = 64 / W;              // key ids per wave
-  static constexpr int kPerStep = 2 * kGroups + 1; // DMA instructions per wave per step
+  // Wave 0 also moves the 64 key ids (one DMA, issued first); the step wait
+  // counts only the tile DMAs, which for wave 0 also covers its id DMA of the
+  // stage issued one step earlier.
+  static constexpr int kPerStep = 2 * kGroups;
 };
 
 // DMA of keys kb .. kb+63 (K rows, V rows, canonical ids) into one stage.
+// kid_row must hold at least kb + 64 entries (the plan pads ids to whole tiles).
 template <int W>
 __device__ __forceinline__ void kv_dma(const char* kg, const char* vg, size_t row_stride, int S,
                                        const int* kid_row, int kb, int wave, char* stage) {
+  if (wave == 0) dma_word64(kid_row + kb + __lane_id(), stage + 2 * kTileBytes);
 #pragma unroll
   for (int j = 0; j < KvDma<W>::kGroups; ++j) {
     const int r0 = 8 * (wave + W * j);
     dma_rows8(kg, row_stride, kb, r0, S - 1, stage);
     dma_rows8(vg, row_stride, kb, r0, S - 1, stage + kTileBytes);
   }
-  constexpr int E = KvDma<W>::kIds;
-  dma_words(kid_row + kb + E * wave, stage + 2 * kTileBytes + 4 * E * wave, E);
 }
 
 }  // namespace mf
