@@ -61,14 +61,18 @@ extern "C" {
 #define MF_TILE 128
 
 /* Offsets (bytes) of the plan's sections, for callers that inspect it:
- * [0] qid int32 [B][nQ*128]   canonical query ids (-1 = inactive)
- * [1] kid int32 [B][nK*128]   canonical key ids   (-2 = inactive)
+ * [0] qid int32 [B][nQ*128]   canonical query ids (segment id; 0 = inactive
+ *                             token or padding past the sequence end)
+ * [1] kid int32 [B][nK*128]   canonical key ids (same convention)
  * [2] tile map uint8 [B][nQ][nK]
  * [3] q_count int32 [B][nQ]    [4] q_list int32 [B][nQ][nK] (kj*4 + class)
  * [5] k_count int32 [B][nK]    [6] k_list int32 [B][nK][nQ] (qi*4 + class)
- * [7] run scratch              [8] total size
+ * [7] q_order int32 [B*nQ]     [8] k_order int32 [B*nK]: the items b*nQ + qi
+ *                              (b*nK + kj) by decreasing list length, the
+ *                              attention kernels' launch order
+ * [9] run scratch              [10] total size
  * with nQ = ceil(T/128), nK = ceil(S/128). */
-void mf_plan_layout(int batch, int q_len, int kv_len, size_t offsets[9]);
+void mf_plan_layout(int batch, int q_len, int kv_len, size_t offsets[11]);
 size_t mf_plan_bytes(int batch, int q_len, int kv_len);
 
 /* Block-mask builder.  Replaces the dense validity grids of

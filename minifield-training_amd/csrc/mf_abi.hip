@@ -83,7 +83,7 @@ int check_attn(int dtype, int batch, int q_len, int kv_len, int q_heads, int kv_
 
 extern "C" {
 
-void mf_plan_layout(int batch, int q_len, int kv_len, size_t offsets[9]) {
+void mf_plan_layout(int batch, int q_len, int kv_len, size_t offsets[11]) {
   const mf::PlanLayout p = mf::plan_layout(batch, q_len, kv_len);
   offsets[0] = p.qid;
   offsets[1] = p.kid;
@@ -92,8 +92,10 @@ void mf_plan_layout(int batch, int q_len, int kv_len, size_t offsets[9]) {
   offsets[4] = p.qlist;
   offsets[5] = p.kcnt;
   offsets[6] = p.klist;
-  offsets[7] = p.runs;
-  offsets[8] = p.total;
+  offsets[7] = p.qorder;
+  offsets[8] = p.korder;
+  offsets[9] = p.runs;
+  offsets[10] = p.total;
 }
 
 size_t mf_plan_bytes(int batch, int q_len, int kv_len) {

@@ -41,6 +41,8 @@ struct BwdArgs {
   const int* qlist;
   const int* kcnt;
   const int* klist;
+  const int* qorder;
+  const int* korder;
   int T, S, Hq, Hkv, G, hchunks;
   int nq, nk, tq_pad, tk_pad;
   int causal;
@@ -188,11 +190,14 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
-  const int hr = blockIdx.x;
-  const int b = uniform(hr / (a.Hkv * a.hchunks));
-  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
+  const int nh = a.Hkv * a.hchunks;
+  const int hr = uniform(blockIdx.x % nh);
+  const int kvh = uniform(hr / a.hchunks);
   const int hc = uniform(hr % a.hchunks);
-  const int qt = uniform(blockIdx.y);
+  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
+  const int b = uniform(item / a.nq);
+  const int qt = uniform(item % a.nq);
   const int qpos = qt * kTile + wave * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
   const bool qvalid = qpos < a.T;
@@ -503,9 +508,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
-  const int b = uniform(blockIdx.x / a.Hkv);
+  // 1-D grid: (key-tile item in launch order, kvh), heads fastest
   const int kvh = uniform(blockIdx.x % a.Hkv);
-  const int kt = uniform(blockIdx.y);
+  const int item = ld_const(a.korder, blockIdx.x / a.Hkv);  // (row, key tile), longest first
+  const int b = uniform(item / a.nk);
+  const int kt = uniform(item % a.nk);
   const int kpos = kt * kTile + wave * 32 + (lane & 31);
   const int mykid = a.kid[(size_t)b * a.tk_pad + kpos];
   const bool kvalid = kpos < a.S;
@@ -687,11 +694,14 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int half = lane >> 5;
-  const int hr = blockIdx.x;
-  const int b = uniform(hr / (a.Hkv * a.hchunks));
-  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
+  const int nh = a.Hkv * a.hchunks;
+  const int hr = uniform(blockIdx.x % nh);
+  const int kvh = uniform(hr / a.hchunks);
   const int hc = uniform(hr % a.hchunks);
-  const int qt = uniform(blockIdx.y);
+  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
+  const int b = uniform(item / a.nq);
+  const int qt = uniform(item % a.nq);
   const int head = kvh * a.G + hc * HPW + (wave >> 2);
   const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
@@ -853,9 +863,11 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   const int wave = uniform(tid >> 6);
   const int half = lane >> 5;
   const int slot = HS == 1 ? 0 : wave >> 2;
-  const int b = uniform(blockIdx.x / a.Hkv);
+  // 1-D grid: (key-tile item in launch order, kvh), heads fastest
   const int kvh = uniform(blockIdx.x % a.Hkv);
-  const int kt = uniform(blockIdx.y);
+  const int item = ld_const(a.korder, blockIdx.x / a.Hkv);  // (row, key tile), longest first
+  const int b = uniform(item / a.nk);
+  const int kt = uniform(item % a.nk);
   const int kpos = kt * kTile + (wave & 3) * 32 + (lane & 31);
   const int mykid = a.kid[(size_t)b * a.tk_pad + kpos];
   const bool kvalid = kpos < a.S;
@@ -1075,6 +1087,8 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   a.qlist = reinterpret_cast<const int*>(p + lay.qlist);
   a.kcnt = reinterpret_cast<const int*>(p + lay.kcnt);
   a.klist = reinterpret_cast<const int*>(p + lay.klist);
+  a.qorder = reinterpret_cast<const int*>(p + lay.qorder);
+  a.korder = reinterpret_cast<const int*>(p + lay.korder);
   a.T = T;
   a.S = S;
   a.Hq = Hq;
@@ -1097,7 +1111,7 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
     else
       hipLaunchKernelGGL((bwd_delta_kernel<false>), dim3(dgrid), dim3(256), 0, stream, a, batch);
   }
-  const dim3 qgrid(batch * Hkv * a.hchunks, lay.nq);
+  const dim3 qgrid(Hkv * a.hchunks * batch * lay.nq);
   if (!(phases & 2)) {
   } else if (f32) {
     if (hpw == 2)
@@ -1110,7 +1124,7 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
     else
       hipLaunchKernelGGL((bwd_dq_bf16_kernel<1>), qgrid, dim3(256), 0, stream, a);
   }
-  const dim3 kgrid(batch * Hkv, lay.nk);
+  const dim3 kgrid(Hkv * batch * lay.nk);
   if (phases & 4) {
     if (f32)
       hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);

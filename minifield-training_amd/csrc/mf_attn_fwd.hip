@@ -31,6 +31,7 @@ struct FwdArgs {
   const int* kid;
   const int* qcnt;
   const int* qlist;
+  const int* qorder;
   int T, S, Hq, Hkv, G, hchunks;
   int nq, nk, tq_pad, tk_pad;
   int causal;
@@ -147,11 +148,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
-  const int hr = blockIdx.x;  // (b, kvh, head chunk)
-  const int b = uniform(hr / (a.Hkv * a.hchunks));
-  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
+  const int nh = a.Hkv * a.hchunks;
+  const int hr = uniform(blockIdx.x % nh);
+  const int kvh = uniform(hr / a.hchunks);
   const int hc = uniform(hr % a.hchunks);
-  const int qt = uniform(blockIdx.y);
+  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
+  const int b = uniform(item / a.nq);
+  const int qt = uniform(item % a.nq);
   const int qpos = qt * kTile + wave * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
   const bool qvalid = qpos < a.T;
@@ -391,11 +395,14 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   // stage arrays, so the compiler sees which stage each DMA writes
   const int wave = uniform(threadIdx.x >> 6);
   const int half = lane >> 5;
-  const int hr = blockIdx.x;  // (b, kvh, head chunk)
-  const int b = uniform(hr / (a.Hkv * a.hchunks));
-  const int kvh = uniform((hr / a.hchunks) % a.Hkv);
+  // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
+  const int nh = a.Hkv * a.hchunks;
+  const int hr = uniform(blockIdx.x % nh);
+  const int kvh = uniform(hr / a.hchunks);
   const int hc = uniform(hr % a.hchunks);
-  const int qt = uniform(blockIdx.y);
+  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
+  const int b = uniform(item / a.nq);
+  const int qt = uniform(item % a.nq);
   const int head = kvh * a.G + hc * HPW + (wave >> 2);
   const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
@@ -593,6 +600,7 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
   a.kid = reinterpret_cast<const int*>(p + lay.kid);
   a.qcnt = reinterpret_cast<const int*>(p + lay.qcnt);
   a.qlist = reinterpret_cast<const int*>(p + lay.qlist);
+  a.qorder = reinterpret_cast<const int*>(p + lay.qorder);
   a.T = T;
   a.S = S;
   a.Hq = Hq;
@@ -607,7 +615,7 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
   a.causal = mode == 0;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
-  const dim3 grid(batch * Hkv * a.hchunks, lay.nq);
+  const dim3 grid(Hkv * a.hchunks * batch * lay.nq);
   if (f32) {
     if (hpw == 2)
       hipLaunchKernelGGL((attn_fwd_kernel<2, true>), grid, dim3(256), 0, stream, a);

@@ -178,6 +178,59 @@ __global__ __launch_bounds__(64) void worklist_kernel(MapArgs a) {
   if (lane == 0) *count = n;
 }
 
+// Launch orders for the attention grids: the (row, tile) items sorted by
+// work-list length, longest first, so that the hardware's in-order dispatch
+// approximates longest-processing-time scheduling and the long tiles do not
+// end up in the last wave of workgroups.  Equal lengths keep index order
+// (the sort is a stable counting sort), so the plan is deterministic.
+// Block 0 orders the query tiles, block 1 the key tiles.  Lengths of
+// kOrderBuckets - 1 and more share the first bucket.
+constexpr int kOrderThreads = 128;
+constexpr int kOrderBuckets = 64;
+
+__device__ __forceinline__ int order_bucket(int len) {
+  return kOrderBuckets - 1 - min(len, kOrderBuckets - 1);
+}
+
+__global__ __launch_bounds__(kOrderThreads) void order_kernel(MapArgs a) {
+  // column t of hist belongs to thread t: counts, then scatter cursors
+  __shared__ int hist[kOrderBuckets][kOrderThreads];
+  __shared__ int part[kOrderThreads];
+  const bool qside = blockIdx.x == 0;
+  const int n = a.batch * (qside ? a.lay.nq : a.lay.nk);
+  const int* len = plan_i32(a.plan, qside ? a.lay.qcnt : a.lay.kcnt);
+  int* order = plan_i32(a.plan, qside ? a.lay.qorder : a.lay.korder);
+  const int t = threadIdx.x;
+  const int per = (n + kOrderThreads - 1) / kOrderThreads;
+  const int lo = min(n, t * per), hi = min(n, lo + per);
+  for (int k = 0; k < kOrderBuckets; ++k) hist[k][t] = 0;
+  for (int i = lo; i < hi; ++i) hist[order_bucket(len[i])][t] += 1;
+  __syncthreads();
+  // exclusive scan of hist in (bucket, thread) order; thread j owns the
+  // kOrderBuckets consecutive entries starting at flat index j * kOrderBuckets
+  static_assert(kOrderBuckets * kOrderThreads % kOrderThreads == 0, "scan split");
+  int* flat = &hist[0][0];
+  constexpr int E = kOrderBuckets;
+  int sum = 0;
+  for (int e = 0; e < E; ++e) sum += flat[t * E + e];
+  part[t] = sum;
+  __syncthreads();
+  for (int step = 1; step < kOrderThreads; step <<= 1) {
+    const int add = t >= step ? part[t - step] : 0;
+    __syncthreads();
+    part[t] += add;
+    __syncthreads();
+  }
+  int base = part[t] - sum;
+  for (int e = 0; e < E; ++e) {
+    const int v = flat[t * E + e];
+    flat[t * E + e] = base;
+    base += v;
+  }
+  __syncthreads();
+  for (int i = lo; i < hi; ++i) order[hist[order_bucket(len[i])][t]++] = i;
+}
+
 hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, int mode,
                             int batch, int q_len, int kv_len, void* plan,
                             hipStream_t stream) {
@@ -197,6 +250,7 @@ hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, i
   hipLaunchKernelGGL(classify_kernel, dim3((a.lay.nq * a.lay.nk + 255) / 256, batch), dim3(256),
                      0, stream, a);
   hipLaunchKernelGGL(worklist_kernel, dim3(a.lay.nq + a.lay.nk, batch), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL(order_kernel, dim3(2), dim3(kOrderThreads), 0, stream, a);
   return hipGetLastError();
 }
 

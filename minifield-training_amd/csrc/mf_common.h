@@ -146,7 +146,7 @@ __device__ __forceinline__ int mask_at(const void* mask, int mask_u8, long idx) 
 
 // Plan section offsets (bytes), shared by host and device code.
 struct PlanLayout {
-  size_t qid, kid, tmap, qcnt, qlist, kcnt, klist, runs, total;
+  size_t qid, kid, tmap, qcnt, qlist, kcnt, klist, qorder, korder, runs, total;
   int nq, nk, tq_pad, tk_pad;
 };
 
@@ -172,6 +172,9 @@ __host__ __device__ inline PlanLayout plan_layout(int batch, int q_len, int kv_l
   p.qlist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nq * p.nk);
   p.kcnt = off;  off = align256(off + sizeof(int) * (size_t)batch * p.nk);
   p.klist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nk * p.nq);
+  // launch orders: (row, tile) items by decreasing work-list length
+  p.qorder = off; off = align256(off + sizeof(int) * (size_t)batch * p.nq);
+  p.korder = off; off = align256(off + sizeof(int) * (size_t)batch * p.nk);
   // run records: q tiles then k tiles, each (count int + kMaxRuns Runs)
   p.runs = off;
   off = align256(off + (sizeof(int) + sizeof(Run) * kMaxRuns) * (size_t)batch * (p.nq + p.nk));

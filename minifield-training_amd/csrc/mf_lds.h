@@ -2,11 +2,17 @@
 //
 // A tile is 64 rows x 128 bytes (64 bf16 of one token and head).  Its 16-byte
 // chunks are XOR-swizzled per row -- chunk c of row r lives at position
-// c ^ swz(r) -- so that
+// c ^ swz(r), with swz a bijection of r & 7 -- so that
 //   * eight consecutive rows read at the same chunk (the 16-byte MFMA operand
-//     reads, lanes r..r+7) hit eight different 16-byte bank groups, and
+//     reads) hit eight different 16-byte bank groups, and
 //   * four consecutive rows read as 32-byte pairs (the transposing reads of
 //     ds_read_b64_tr_b16) hit four different 32-byte bank groups.
+// gfx950's LDS has 64 banks and serves a 16-byte read 16 lanes per clock, so
+// rows r and r + 8 of such a read share a bank group (a 2-way conflict).  A
+// key that also depends on bit 3 of the row removes it, but its row-dependent
+// addresses cost the forward kernel more registers than its budget of 128
+// (spills), which costs far more than the conflict; with swz depending on
+// r & 7 only, every lane's chunk offset is the same for rows 8 apart.
 // A DMA instruction writes lane L's 16 bytes to LDS base + 16 L, so a wave
 // moves 8 rows per instruction; the swizzle is applied on the source side by
 // choosing which global chunk each lane fetches.
@@ -85,10 +91,9 @@ __device__ __forceinline__ bf16x8 tile_chunk(const char* tile, int r, int c) {
 // column col (a multiple of 4), read with ds_read_b64_tr_b16.
 __device__ __forceinline__ bf16x8 tile_tr_operand(const char* tile, int row, int col) {
   const int c = col >> 3, within = (col & 7) * 2;
-  // swz(row + 8) == swz(row): the second read is 8 rows (1 KiB) further on
-  const char* p = tile + row * kRowBytes + ((c ^ swz(row)) << 4) + within;
+  const char* p = tile + chunk_off(row, c) + within;
   const u32x2 lo = lds_read_tr16(p);
-  const u32x2 hi = lds_read_tr16(p + 8 * kRowBytes);
+  const u32x2 hi = lds_read_tr16(p + 8 * kRowBytes);  // swz(row + 8) == swz(row)
   const u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
   return __builtin_bit_cast(bf16x8, w);
 }

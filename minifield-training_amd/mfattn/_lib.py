@@ -125,7 +125,7 @@ def check(rc: int) -> None:
 
 
 def plan_layout(batch: int, q_len: int, kv_len: int) -> list[int]:
-    out = (ctypes.c_size_t * 9)()
+    out = (ctypes.c_size_t * 11)()
     LIB.mf_plan_layout(batch, q_len, kv_len, out)
     return list(out)
 

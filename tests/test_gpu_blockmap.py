@@ -42,6 +42,11 @@ def _check(mode, mask, seg, t, s, device):
             nz = np.flatnonzero(tm[r, :, kj])
             assert kcnt[r, kj] == nz.size
             np.testing.assert_array_equal(klist[r, kj, : nz.size], nz * 4 + tm[r, nz, kj])
+    # launch orders: items by decreasing list length (lengths >= 63 tie), stable
+    for sec, cnt in ((7, qcnt), (8, kcnt)):
+        order = plan.section(sec, torch.int32, (cnt.size,)).cpu().numpy()
+        want = np.argsort(63 - np.minimum(cnt.ravel(), 63), kind="stable")
+        np.testing.assert_array_equal(order, want)
     qid, kid = masks._token_ids(mode, mask, seg, t)
     gq = plan.section(0, torch.int32, (b, nq * 128)).cpu().numpy()
     gk = plan.section(1, torch.int32, (b, nk * 128)).cpu().numpy()
