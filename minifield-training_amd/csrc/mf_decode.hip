@@ -265,6 +265,181 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 decode: one wave per (row, 256-token chunk, KV head) item, no LDS.
+// Lane = (key kg = lane / 8 of an 8-key group, d-slice dl = lane % 8 of 8
+// dims), so one 16-byte load per lane covers 8 whole 128-byte key rows and a
+// wave streams 32 keys of K and V (8 KiB) per iteration, the next
+// iteration's loads in flight while this one is scored.  Scores are 4-term
+// bf16 dot products (v_dot2) reduced over the 8 lanes of a key with DPP;
+// P V packs pairs of probabilities and the matching V elements of two keys
+// into bf16 pairs for v_dot2 as well.  The online softmax keeps one running
+// max per query head (wave-uniform) and rescales lazily like the prefill
+// forward.  The chunk's (max, sum, unnormalised output) go to the same
+// partial buffer the combine kernel reads.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// sum over the 8 lanes of a key group (lanes 8j .. 8j+7)
+__device__ __forceinline__ float group8_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));  // quad xor 1
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, false));  // quad xor 2
+  x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xF, 0xF, false)); // half-row mirror
+  return x;
+}
+
+// combine over the 8 key groups (lanes with equal lane % 8): the lane ^ 8,
+// lane ^ 16 and lane ^ 32 exchanges
+template <bool MAX>
+__device__ __forceinline__ float across_groups(float x) {
+  const float m = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xF, 0xF, false));  // row_ror:8 = lane ^ 8 in a row of 16
+  x = MAX ? fmaxf(x, m) : x + m;
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = MAX ? fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]))
+          : __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return MAX ? fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]))
+             : __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+constexpr int kDecChunk = 256;  // tokens per work item (bf16)
+
+template <int G>
+__global__ __launch_bounds__(256) void decode_bf16_kernel(DecArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int kg = lane >> 3, dl = lane & 7;
+  const int total = ld_const(a.offsets, a.B) * a.Hkv;
+  const int nwaves = gridDim.x * 4;
+  const float c = a.scale_log2;
+  const float tau = 8.f / c;
+  const bf16* ks = reinterpret_cast<const bf16*>(a.k);
+  const bf16* vs = reinterpret_cast<const bf16*>(a.v);
+
+  for (int item = uniform(blockIdx.x * 4 + (threadIdx.x >> 6)); item < total; item += nwaves) {
+    const int kvh = item % a.Hkv;
+    const int ci = item / a.Hkv;  // chunk item over all rows
+    int lo = 0, hi = a.B - 1;     // row: last b with offsets[b] <= ci
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (ld_const(a.offsets, mid) <= ci) lo = mid; else hi = mid - 1;
+    }
+    const int b = uniform(lo);
+    const int chunk = ci - ld_const(a.offsets, b);
+    const int raw = ld_const(a.lengths, b);
+    const bool flat = raw <= 0;  // every slot masked: uniform weights
+    const int len = eff_len(raw, a.cap);
+    const int t0 = chunk * kDecChunk;
+    const int n = min(kDecChunk, len - t0);
+    const int last = t0 + n - 1;
+
+    u32x4 qv[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      qv[g] = ld_u32x4(reinterpret_cast<const bf16*>(a.q) + ((size_t)b * a.Hq + kvh * G + g) * kD + 8 * dl);
+    const size_t head_off = (size_t)kvh * kD + 8 * dl;
+    auto row_ptr = [&](const bf16* base, int t) {
+      return base + ((size_t)b * a.cap + min(t, last)) * a.Hkv * kD + head_off;
+    };
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = kNegInf;
+      l[g] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    }
+    const int iters = (n + 31) >> 5;
+    u32x4 kc[4], vc[4], kn[4], vn[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      kc[u] = ld_u32x4(row_ptr(ks, t0 + 8 * u + kg));
+      vc[u] = ld_u32x4(row_ptr(vs, t0 + 8 * u + kg));
+    }
+    for (int it = 0; it < iters; ++it) {
+      const int tb = t0 + 32 * it;
+      // prefetch the next 32 keys (clamped into the chunk, so always in bounds)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kn[u] = ld_u32x4(row_ptr(ks, tb + 32 + 8 * u + kg));
+        vn[u] = ld_u32x4(row_ptr(vs, tb + 32 + 8 * u + kg));
+      }
+      float s[G][4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool valid = tb + 8 * u + kg <= last;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float x = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) x = dot2_bf16(qv[g][j], kc[u][j], x);
+          x = group8_sum(x);
+          s[g][u] = valid ? (flat ? 0.f : x) : kNegInf;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mx = fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3]));
+        mx = across_groups<true>(mx);
+        if (mx > m[g] + tau) {  // wave-uniform
+          const float alpha = m[g] == kNegInf ? 0.f : fast_exp2((m[g] - mx) * c);
+          m[g] = mx;
+          l[g] *= alpha;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+        }
+        const float mc = m[g] * c;
+        float p[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          p[u] = fast_exp2(fmaf(s[g][u], c, -mc));
+          l[g] += p[u];
+        }
+        // P V: bf16 pairs over keys (u, u + 1)
+#pragma unroll
+        for (int up = 0; up < 2; ++up) {
+          const bf16x2_t pp = {(bf16)p[2 * up], (bf16)p[2 * up + 1]};
+          const uint32_t pw = __builtin_bit_cast(uint32_t, pp);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const uint32_t va = vc[2 * up][j], vb = vc[2 * up + 1][j];
+            // (va.lo, vb.lo) and (va.hi, vb.hi)
+            const uint32_t lo16 = __builtin_amdgcn_perm(vb, va, 0x05040100u);
+            const uint32_t hi16 = __builtin_amdgcn_perm(vb, va, 0x07060302u);
+            acc[g][2 * j] = dot2_bf16(pw, lo16, acc[g][2 * j]);
+            acc[g][2 * j + 1] = dot2_bf16(pw, hi16, acc[g][2 * j + 1]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kc[u] = kn[u];
+        vc[u] = vn[u];
+      }
+    }
+    // reduce over the 8 key groups; lanes 0..7 hold the chunk's result
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float lt = across_groups<false>(l[g]);
+      const int h = kvh * G + g;
+      float* dst = a.partial + (((size_t)b * a.Hq + h) * a.maxc + chunk) * (2 + kD);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float o = across_groups<false>(acc[g][i]);
+        if (kg == 0) dst[2 + 8 * dl + i] = o;
+      }
+      if (lane == 0) {
+        dst[0] = m[g] * c;
+        dst[1] = lt;
+      }
+    }
+  }
+}
+
 // One wave per (row, query head): lane = d.
 template <bool F32>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
@@ -292,7 +467,7 @@ size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk) {
          sizeof(float) * (size_t)batch * Hq * maxc * (2 + kD);
 }
 
-int decode_chunk(bool f32) { return f32 ? 128 : 256; }
+int decode_chunk(bool f32) { return f32 ? 128 : kDecChunk; }
 
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
                          bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
@@ -322,10 +497,20 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
   if (f32) {
     hipLaunchKernelGGL((decode_kernel<true>), dim3(gx, Hkv), dim3(256), 0, stream, a);
     hipLaunchKernelGGL((decode_combine_kernel<true>), dim3(batch * Hq), dim3(64), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((decode_kernel<false>), dim3(gx, Hkv), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL((decode_combine_kernel<false>), dim3(batch * Hq), dim3(64), 0, stream, a);
+    return hipGetLastError();
   }
+  // bf16: persistent grid of 4-wave blocks over (chunk item, KV head)
+  const int items = upper * Hkv;
+  int blocks = (items + 3) / 4;
+  if (blocks > 2048) blocks = 2048;
+  switch (a.G) {
+    case 1: hipLaunchKernelGGL((decode_bf16_kernel<1>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((decode_bf16_kernel<2>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((decode_bf16_kernel<4>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL((decode_bf16_kernel<8>), dim3(blocks), dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((decode_kernel<false>), dim3(gx, Hkv), dim3(256), 0, stream, a); break;
+  }
+  hipLaunchKernelGGL((decode_combine_kernel<false>), dim3(batch * Hq), dim3(64), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -31,12 +31,22 @@ def test_reference_cached_fixture(device):
     assert out.shape == (2, 1, 4, 8)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_ragged_lengths_and_edges(dtype, device):
+@pytest.mark.parametrize("dtype,hq,hkv", [
+    (torch.float32, 8, 2),
+    (torch.bfloat16, 8, 2),   # 4 query heads per KV head
+    (torch.bfloat16, 2, 2),   # 1
+    (torch.bfloat16, 4, 2),   # 2
+    (torch.bfloat16, 6, 2),   # 3: served by the LDS-staged kernel
+    (torch.bfloat16, 16, 2),  # 8
+])
+def test_ragged_lengths_and_edges(dtype, hq, hkv, device):
     rng = np.random.default_rng(5)
-    b, cap, hq, hkv = 7, 1000, 8, 2
-    say("decode ragged", dtype)
-    lengths = np.array([1, 999, 1000, 1500, 0, 257, 128], np.int32)
+    b, cap = 7, 1000
+    say("decode ragged", dtype, "hq", hq, "hkv", hkv)
+    # 1 token, chunk and 32-key boundaries (256, 257, 31, 33), full and
+    # over-full rows, and a length of 0 (uniform average over the capacity)
+    lengths = np.array([1, 999, 1000, 1500, 0, 257, 31, 33, 256, -3], np.int32)
+    b = lengths.size
     q = rng.standard_normal((b, 1, hq, 64)).astype(np.float32)
     k = rng.standard_normal((b, cap, hkv, 64)).astype(np.float32)
     v = rng.standard_normal((b, cap, hkv, 64)).astype(np.float32)
