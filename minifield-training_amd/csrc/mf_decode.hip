@@ -440,7 +440,9 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(DecArgs a) {
   }
 }
 
-// One wave per (row, query head): lane = d.
+// One wave per (row, query head).  The chunk maxima and sums are combined
+// lane-parallel over chunks; the outputs with lane = d, loading the chunks'
+// partial outputs independently of each other.
 template <bool F32>
 __global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
   const int bh = blockIdx.x;
@@ -449,13 +451,16 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
   const int nch = a.offsets[b + 1] - a.offsets[b];
   const float* src = a.partial + (size_t)bh * a.maxc * (2 + kD);
   float M = kNegInf;
-  for (int ch = 0; ch < nch; ++ch) M = fmaxf(M, src[ch * (2 + kD)]);
-  float L = 0.f, acc = 0.f;
-  for (int ch = 0; ch < nch; ++ch) {
-    const float w = fast_exp2(src[ch * (2 + kD)] - M);
-    L = fmaf(src[ch * (2 + kD) + 1], w, L);
-    acc = fmaf(src[ch * (2 + kD) + 2 + lane], w, acc);
-  }
+  for (int ch = lane; ch < nch; ch += 64) M = fmaxf(M, src[ch * (2 + kD)]);
+  M = wave_max(M);
+  float L = 0.f;
+  for (int ch = lane; ch < nch; ch += 64)
+    L = fmaf(src[ch * (2 + kD) + 1], fast_exp2(src[ch * (2 + kD)] - M), L);
+  L = wave_sum(L);
+  float acc = 0.f;
+#pragma unroll 4
+  for (int ch = 0; ch < nch; ++ch)
+    acc = fmaf(src[ch * (2 + kD) + 2 + lane], fast_exp2(src[ch * (2 + kD)] - M), acc);
   const float o = acc / L;
   if constexpr (!F32) reinterpret_cast<bf16*>(a.out)[(size_t)bh * kD + lane] = (bf16)o;
   else reinterpret_cast<float*>(a.out)[(size_t)bh * kD + lane] = o;
