@@ -59,14 +59,15 @@ def _time_calls(fn, iters):
 
 
 def _traffic(kernel: str, workload: str):
+    """HBM bytes per launch from the committed PMC summary, or None."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
         return None
-    data = json.loads(path.read_text())
-    return data.get(workload, {}).get(kernel)
+    entry = json.loads(path.read_text()).get(workload, {}).get(kernel)
+    return None if entry is None else entry["bytes"]
 
 
-def gpu_leg(steps: int, warmup: int):
+def gpu_leg(steps: int, warmup: int, profile: bool = False):
     import numpy as np
     import torch
 
@@ -97,6 +98,13 @@ def gpu_leg(steps: int, warmup: int):
         ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, scale, ws, dq)
         ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv)
 
+    if profile:  # one step and one decode for the PMC passes, untimed
+        step()
+        torch.cuda.synchronize()
+        del q, k, v, do, dq, dk, dv, ws
+        torch.cuda.empty_cache()
+        decode_leg(0, 0, profile=True)
+        return None
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -110,20 +118,26 @@ def gpu_leg(steps: int, warmup: int):
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     ms = start.elapsed_time(end) / steps
 
-    # per-kernel durations (HIP events on the launch stream)
-    plan = ops.block_map(seg, mask, mode, w.length, w.length)
-    out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
-    ops.attn_bwd_delta(out, do, ws)
+    # per-kernel durations: HIP events on the launch stream between the
+    # launches of a step, over as many steps as were timed, so every kernel
+    # runs in the same order and cache state as in the timed loop
+    names = ("block_map", "attn_fwd", "attn_bwd_delta", "attn_bwd_dq", "attn_bwd_dkdv")
+    marks = [_events(len(names) + 1) for _ in range(steps)]
+    for ev in marks:
+        ev[0].record()
+        plan = ops.block_map(seg, mask, mode, w.length, w.length)
+        ev[1].record()
+        out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
+        ev[2].record()
+        ops.attn_bwd_delta(out, do, ws)
+        ev[3].record()
+        ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, scale, ws, dq)
+        ev[4].record()
+        ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv)
+        ev[5].record()
     torch.cuda.synchronize()
-    iters = max(steps, 5)
-    kern = {
-        "block_map": _time_calls(lambda: ops.block_map(seg, mask, mode, w.length, w.length), iters),
-        "attn_fwd": _time_calls(lambda: ops.attn_fwd(q, k, v, plan, mode, scale), iters),
-        "attn_bwd_delta": _time_calls(lambda: ops.attn_bwd_delta(out, do, ws), iters),
-        "attn_bwd_dq": _time_calls(lambda: ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, scale, ws, dq), iters),
-        "attn_bwd_dkdv": _time_calls(
-            lambda: ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv), iters),
-    }
+    kern = {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in marks) / steps
+            for i, name in enumerate(names)}
     flops = workloads.attention_flops(w)
     algo = {"attn_fwd": flops["fwd"], "attn_bwd_dq": flops["dq"], "attn_bwd_dkdv": flops["dkdv"]}
     dominant = max(algo, key=lambda name: kern[name])
@@ -152,7 +166,7 @@ def gpu_leg(steps: int, warmup: int):
     return result
 
 
-def decode_leg(steps: int, warmup: int):
+def decode_leg(steps: int, warmup: int, profile: bool = False):
     import torch
 
     from mfattn import ops, workloads
@@ -168,6 +182,10 @@ def decode_leg(steps: int, warmup: int):
     lengths = torch.tensor(d.valid_length, device=dev)
     scale = d.head_dim ** -0.5
     run = lambda: ops.decode(q, kc, vc, lengths, scale)  # noqa: E731
+    if profile:
+        run()
+        torch.cuda.synchronize()
+        return None
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
@@ -228,6 +246,83 @@ def cpu_leg(seconds: float):
                       "FLOPs of the chunks / time"}
 
 
+# --------------------------------------------------------------------------
+# HBM traffic of the measured kernels (rocprofv3 PMC passes)
+#
+#   cd /tmp && export TMPDIR=/tmp
+#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d <root>/gpurun_out/pmc_fetch -o run \
+#       -- python3 <root>/bench.py --profile-step
+#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d <root>/gpurun_out/pmc_write -o run \
+#       -- python3 <root>/bench.py --profile-step
+#   python3 bench.py --traffic gpurun_out/pmc_fetch gpurun_out/pmc_write
+#
+# --profile-step runs one device-to-device copy of CALIB_BYTES (the
+# calibration: it reads and writes exactly that many bytes), one C2 step and
+# one C4 decode.  --traffic scales each kernel's FETCH_SIZE / WRITE_SIZE
+# (KiB per dispatch) by what the counters read for the copy and writes
+# profiles/traffic.json, which the timed run reports as roofline.traffic.
+# --------------------------------------------------------------------------
+CALIB_BYTES = 512 << 20
+TRAFFIC_KERNELS = {  # bench name -> device kernel (C2: bf16, 2 heads per KV head)
+    "block_map": ("mf::token_ids_kernel", "mf::tile_runs_kernel", "mf::classify_kernel",
+                  "mf::worklist_kernel", "mf::order_kernel"),
+    "attn_fwd": ("mf::attn_fwd_bf16_kernel<2>",),
+    "attn_bwd_delta": ("mf::bwd_delta_kernel<false>",),
+    "attn_bwd_dq": ("mf::bwd_dq_bf16_kernel<2>",),
+    "attn_bwd_dkdv": ("mf::bwd_dkdv_bf16_kernel<2>",),
+    "decode": ("mf::decode_prep_kernel", "mf::decode_bf16_kernel<2>", "mf::decode_combine_kernel<false>"),
+}
+
+
+def profile_step() -> None:
+    import torch
+
+    src = torch.empty(CALIB_BYTES // 2, dtype=torch.bfloat16, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    gpu_leg(1, 0, profile=True)
+
+
+def _counter_means(path: pathlib.Path) -> dict:
+    import csv
+    import re
+
+    sums, counts = {}, {}
+    for row in csv.DictReader(open(path)):
+        name = re.sub(r"\(.*", "", row["Kernel_Name"]).replace("void ", "").strip()
+        key = (name, int(row.get("Dispatch_Id", 0) or 0))
+        sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
+    per_kernel = {}
+    for (name, _), value in sums.items():
+        per_kernel.setdefault(name, []).append(value)
+    return {name: sum(v) / len(v) for name, v in per_kernel.items()} | {
+        "__calls__": {name: len(v) for name, v in per_kernel.items()}}
+
+
+def traffic_from(fetch_dir: str, write_dir: str) -> dict:
+    fetch = _counter_means(next(pathlib.Path(fetch_dir).rglob("*counter_collection.csv")))
+    write = _counter_means(next(pathlib.Path(write_dir).rglob("*counter_collection.csv")))
+    copy = "__amd_rocclr_copyBuffer"
+    calls_f, calls_w = fetch["__calls__"].get(copy, 1), write["__calls__"].get(copy, 1)
+    f_scale = CALIB_BYTES / (fetch[copy] * calls_f * 1024)
+    w_scale = CALIB_BYTES / (write[copy] * calls_w * 1024)
+    out = {"calibration": {"copy_bytes": CALIB_BYTES, "fetch_kib_per_copy": fetch[copy] * calls_f,
+                           "write_kib_per_copy": write[copy] * calls_w,
+                           "fetch_scale": f_scale, "write_scale": w_scale}}
+    for name, kernels in TRAFFIC_KERNELS.items():
+        fb = sum(fetch.get(k, 0.0) for k in kernels) * 1024 * f_scale
+        wb = sum(write.get(k, 0.0) for k in kernels) * 1024 * w_scale
+        workload = "C4" if name == "decode" else "C2"
+        out.setdefault(workload, {})[name] = {"fetch_bytes": fb, "write_bytes": wb,
+                                              "bytes": fb + wb}
+    (ROOT / "profiles").mkdir(exist_ok=True)
+    (ROOT / "profiles" / "traffic.json").write_text(json.dumps(out, indent=1) + "\n")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -235,7 +330,17 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-step", action="store_true",
+                    help="run the calibration copy, one C2 step and one C4 decode (for rocprofv3 --pmc)")
+    ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two PMC runs of --profile-step into profiles/traffic.json")
     args = ap.parse_args()
+    if args.traffic:
+        print(json.dumps(traffic_from(*args.traffic), indent=1))
+        return 0
+    if args.profile_step:
+        profile_step()
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
               "(the packed-attention path has no cross-GPU work in this build)", file=sys.stderr)
