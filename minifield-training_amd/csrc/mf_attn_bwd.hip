@@ -686,7 +686,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
 // transposing LDS reads.
 // ---------------------------------------------------------------------------
 template <int HPW>
-__global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(4)))
 void bwd_dq_bf16_kernel(BwdArgs a) {
   constexpr int W = 4 * HPW;
   __shared__ __attribute__((aligned(16))) char stage0[kStageBytes], stage1[kStageBytes],
@@ -742,6 +742,48 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage);
   };
 
+  // Sub-block classification inside PARTIAL tiles, as in the forward: a
+  // wave's 32 queries against one 32-key block are skipped when no pair can
+  // be valid and run without id masks when every id matches.
+  const int q0 = qt * kTile + (wave & 3) * 32;
+  const int u = uniform(myqid);
+  const bool quni = __all(myqid == u);
+
+  auto block = [&](const char* kt, const char* vt, const int* kids_lds, int kb, int kb2,
+                   bool mask_ids, bool diag) {
+    f32x16 s = zero16(), dp = zero16();
+    const int krow = kb2 * 32 + (lane & 31);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      s = mfma32x32x16(tile_chunk(kt, krow, 2 * ks + half), qf[ks], s);
+      dp = mfma32x32x16(tile_chunk(vt, krow, 2 * ks + half), gf[ks], dp);
+    }
+    if (mask_ids) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int4 kids = *reinterpret_cast<const int4*>(&kids_lds[kb2 * 32 + 8 * g4 + 4 * half]);
+        const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[g4 * 4 + i] = kv[i] == myqid ? s[g4 * 4 + i] : kNegInf;
+      }
+    }
+    if (diag) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        s[r] = kb + kb2 * 32 + acc_row(r, lane) <= qpos ? s[r] : kNegInf;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], c, -lse2)) * (dp[r] - dlt);
+    const bf16x8 ds0 = pack8(s, 0), ds1 = pack8(s, 8);
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const bf16x8 k0 = tile_tr_operand(kt, kb2 * 32 + tr_row, db * 32 + tr_col);
+      const bf16x8 k1 = tile_tr_operand(kt, kb2 * 32 + 16 + tr_row, db * 32 + tr_col);
+      dqacc[db] = mfma32x32x16(k0, ds0, dqacc[db]);
+      dqacc[db] = mfma32x32x16(k1, ds1, dqacc[db]);
+    }
+  };
+
   auto compute = [&](int step, const char* stage) {
     const int entry = ld_const(list, step >> 1);
     const int kb = (entry >> 2) * kTile + (step & 1) * kKvStep;
@@ -751,38 +793,21 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     const int* kids_lds = reinterpret_cast<const int*>(stage + 2 * kTileBytes);
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
-      f32x16 s = zero16(), dp = zero16();
-      const int krow = kb2 * 32 + (lane & 31);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        s = mfma32x32x16(tile_chunk(kt, krow, 2 * ks + half), qf[ks], s);
-        dp = mfma32x32x16(tile_chunk(vt, krow, 2 * ks + half), gf[ks], dp);
-      }
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        bool ok[4] = {true, true, true, true};
-        if (partial) {
-          const int kk0 = kb2 * 32 + 8 * g4 + 4 * half;
-          const int4 kids = *reinterpret_cast<const int4*>(&kids_lds[kk0]);
-          const int kv[4] = {kids.x, kids.y, kids.z, kids.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ok[i] = kv[i] == myqid && (!a.causal || kb + kk0 + i <= qpos);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = g4 * 4 + i;
-          const float p = ok[i] ? fast_exp2(fmaf(s[r], c, -lse2)) : 0.f;
-          s[r] = p * (dp[r] - dlt);
+      bool run = true, mask_ids = false, diag = false;
+      if (partial) {
+        const int k0 = kb + kb2 * 32;
+        const bool above = a.causal && k0 > q0 + 31;
+        diag = a.causal && k0 + 31 > q0;
+        if (quni) {
+          const uint64_t m = __ballot(kids_lds[kb2 * 32 + (lane & 31)] == u);
+          run = !above && u != 0 && m != 0;
+          mask_ids = m != ~0ull;
+        } else {
+          run = !above;
+          mask_ids = true;
         }
       }
-      const bf16x8 ds0 = pack8(s, 0), ds1 = pack8(s, 8);
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const bf16x8 k0 = tile_tr_operand(kt, kb2 * 32 + tr_row, db * 32 + tr_col);
-        const bf16x8 k1 = tile_tr_operand(kt, kb2 * 32 + 16 + tr_row, db * 32 + tr_col);
-        dqacc[db] = mfma32x32x16(k0, ds0, dqacc[db]);
-        dqacc[db] = mfma32x32x16(k1, ds1, dqacc[db]);
-      }
+      if (run) block(kt, vt, kids_lds, kb, kb2, mask_ids, diag);
     }
   };
 
