@@ -953,69 +953,97 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     }
   };
 
+  // Sub-block classification inside PARTIAL tiles (mirror of the forward's,
+  // with the roles of queries and keys swapped): the wave's 32 keys against
+  // one 32-query block are skipped when no pair can be valid and run without
+  // id masks when every id matches.
+  const int k0 = kt * kTile + (wave & 3) * 32;
+  const int uk = uniform(mykid);
+  const bool kuni = __all(mykid == uk);
+
+  auto block = [&](const char* qt, const char* gt, const float* lse_l, const float* dlt_l,
+                   const int* qid_l, int qb, int qb2, bool mask_ids, bool diag) {
+    f32x16 s = zero16(), dp = zero16();
+    const int qrow = qb2 * 32 + (lane & 31);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      s = mfma32x32x16(tile_chunk(qt, qrow, 2 * ks + half), kf[ks], s);
+      dp = mfma32x32x16(tile_chunk(gt, qrow, 2 * ks + half), vf[ks], dp);
+    }
+    if (mask_ids) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int4 ids = *reinterpret_cast<const int4*>(&qid_l[qb2 * 32 + 8 * g4 + 4 * half]);
+        const int iv[4] = {ids.x, ids.y, ids.z, ids.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[g4 * 4 + i] = iv[i] == mykid ? s[g4 * 4 + i] : kNegInf;
+      }
+    }
+    if (diag) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        s[r] = kpos <= qb + qb2 * 32 + acc_row(r, lane) ? s[r] : kNegInf;
+    }
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int qq0 = qb2 * 32 + 8 * g4 + 4 * half;
+      const float4 l4 = *reinterpret_cast<const float4*>(&lse_l[qq0]);
+      const float4 d4 = *reinterpret_cast<const float4*>(&dlt_l[qq0]);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = g4 * 4 + i;
+        // masked scores are -inf and inactive rows have lse = +inf: p = 0
+        const float p = fast_exp2(fmaf(s[r], c, -lv[i] * kLog2e));
+        s[r] = p;
+        dp[r] = p * (dp[r] - dv4[i]);
+      }
+    }
+    const bf16x8 pf0 = pack8(s, 0), pf1 = pack8(s, 8);
+    const bf16x8 sf0 = pack8(dp, 0), sf1 = pack8(dp, 8);
+    const int r0 = qb2 * 32 + tr_row_of(lane);
+    const int cb = tr_col_of(lane);
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      const bf16x8 g0 = tile_tr_operand(gt, r0, db * 32 + cb);
+      const bf16x8 g1 = tile_tr_operand(gt, r0 + 16, db * 32 + cb);
+      dvacc[db] = mfma32x32x16(g0, pf0, dvacc[db]);
+      dvacc[db] = mfma32x32x16(g1, pf1, dvacc[db]);
+      const bf16x8 q0 = tile_tr_operand(qt, r0, db * 32 + cb);
+      const bf16x8 q1 = tile_tr_operand(qt, r0 + 16, db * 32 + cb);
+      dkacc[db] = mfma32x32x16(q0, sf0, dkacc[db]);
+      dkacc[db] = mfma32x32x16(q1, sf1, dkacc[db]);
+    }
+  };
+
   auto compute = [&](int it, const char* stage) {
     const int entry = ld_const(list, it / per_tile);
     const int rem = it % per_tile;
     const int qb = (entry >> 2) * kTile + (rem & 1) * kKvStep;
     const bool partial = (entry & 3) == 1;
-    // a select between constant offsets (not slot * size) keeps the tile
-    // addresses analysable, so the compiler can tell these reads from the
-    // DMAs in flight to the other stages and inserts no wait for them
-    const char* qt = slot ? stage + 2 * kTileBytes : stage;
-    const char* gt = slot ? stage + 3 * kTileBytes : stage + kTileBytes;
+    const char* qt = stage + 2 * slot * kTileBytes;
+    const char* gt = stage + (2 * slot + 1) * kTileBytes;
     const float* lse_l = reinterpret_cast<const float*>(stage + Q::kLseOff + slot * 256);
     const float* dlt_l = reinterpret_cast<const float*>(stage + Q::kDltOff + slot * 256);
     const int* qid_l = reinterpret_cast<const int*>(stage + Q::kIdOff);
-    const int tr_row = tr_row_of(lane);
-    const int tr_col = tr_col_of(lane);
-    // Fully unrolled: an inner loop header here would make the compiler's
-    // wait insertion give up tracking which LDS stage each DMA in flight
-    // targets and wait for all of them (vmcnt(0)).
 #pragma unroll
     for (int qb2 = 0; qb2 < 2; ++qb2) {
-      f32x16 s = zero16(), dp = zero16();
-      const int qrow = qb2 * 32 + (lane & 31);
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        s = mfma32x32x16(tile_chunk(qt, qrow, 2 * ks + half), kf[ks], s);
-        dp = mfma32x32x16(tile_chunk(gt, qrow, 2 * ks + half), vf[ks], dp);
-      }
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const int qq0 = qb2 * 32 + 8 * g4 + 4 * half;
-        const float4 l4 = *reinterpret_cast<const float4*>(&lse_l[qq0]);
-        const float4 d4 = *reinterpret_cast<const float4*>(&dlt_l[qq0]);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-        bool ok[4] = {true, true, true, true};
-        if (partial) {
-          const int4 ids = *reinterpret_cast<const int4*>(&qid_l[qq0]);
-          const int iv[4] = {ids.x, ids.y, ids.z, ids.w};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ok[i] = iv[i] == mykid && (!a.causal || kpos <= qb + qq0 + i);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = g4 * 4 + i;
-          const float p = ok[i] ? fast_exp2(fmaf(s[r], c, -lv[i] * kLog2e)) : 0.f;
-          s[r] = p;
-          dp[r] = p * (dp[r] - dv4[i]);
+      bool run = true, mask_ids = false, diag = false;
+      if (partial) {
+        const int q0 = qb + qb2 * 32;
+        const bool above = a.causal && k0 > q0 + 31;
+        diag = a.causal && k0 + 31 > q0;
+        if (kuni) {
+          const uint64_t m = __ballot(qid_l[qb2 * 32 + (lane & 31)] == uk);
+          run = !above && uk != 0 && m != 0;
+          mask_ids = m != ~0ull;
+        } else {
+          run = !above;
+          mask_ids = true;
         }
       }
-      const bf16x8 pf0 = pack8(s, 0), pf1 = pack8(s, 8);
-      const bf16x8 sf0 = pack8(dp, 0), sf1 = pack8(dp, 8);
-      const int r0 = qb2 * 32 + tr_row;
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const bf16x8 g0 = tile_tr_operand(gt, r0, db * 32 + tr_col);
-        const bf16x8 g1 = tile_tr_operand(gt, r0 + 16, db * 32 + tr_col);
-        dvacc[db] = mfma32x32x16(g0, pf0, dvacc[db]);
-        dvacc[db] = mfma32x32x16(g1, pf1, dvacc[db]);
-        const bf16x8 q0 = tile_tr_operand(qt, r0, db * 32 + tr_col);
-        const bf16x8 q1 = tile_tr_operand(qt, r0 + 16, db * 32 + tr_col);
-        dkacc[db] = mfma32x32x16(q0, sf0, dkacc[db]);
-        dkacc[db] = mfma32x32x16(q1, sf1, dkacc[db]);
-      }
+      if (run) block(qt, gt, lse_l, dlt_l, qid_l, qb, qb2, mask_ids, diag);
     }
   };
 
@@ -1151,10 +1179,11 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   }
   const dim3 kgrid(Hkv * batch * lay.nk);
   if (phases & 4) {
+    // One head slot (4-wave workgroups, two per CU): measured 11-32% faster
+    // than two slots in one 8-wave workgroup at C2/C3/C5, because the two
+    // workgroups of a CU do not share barriers.
     if (f32)
       hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);
-    else if (a.G % 2 == 0)
-      hipLaunchKernelGGL((bwd_dkdv_bf16_kernel<2>), kgrid, dim3(512), 0, stream, a);
     else
       hipLaunchKernelGGL((bwd_dkdv_bf16_kernel<1>), kgrid, dim3(256), 0, stream, a);
   }
