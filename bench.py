@@ -92,11 +92,11 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False):
     ws = ops.bwd_workspace(q)
 
     def step():
+        # the product path: block map, forward, one backward call (mf_attn_bwd:
+        # dq with D fused in, then dk/dv)
         plan = ops.block_map(seg, mask, mode, w.length, w.length)
         out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
-        ops.attn_bwd_delta(out, do, ws)
-        ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, scale, ws, dq)
-        ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv)
+        ops.attn_bwd(q, k, v, out, do, lse, plan, mode, scale)
 
     if profile:  # one step and one decode for the PMC passes, untimed
         step()
@@ -120,7 +120,9 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False):
 
     # per-kernel durations: HIP events on the launch stream between the
     # launches of a step, over as many steps as were timed, so every kernel
-    # runs in the same order and cache state as in the timed loop
+    # runs in the same order and cache state as in the timed loop.  The
+    # backward runs as its three phase entry points here (D by its own
+    # kernel, dq reading it); the timed step fuses D into dq instead.
     names = ("block_map", "attn_fwd", "attn_bwd_delta", "attn_bwd_dq", "attn_bwd_dkdv")
     marks = [_events(len(names) + 1) for _ in range(steps)]
     for ev in marks:

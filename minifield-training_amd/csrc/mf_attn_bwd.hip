@@ -46,6 +46,7 @@ struct BwdArgs {
   int T, S, Hq, Hkv, G, hchunks;
   int nq, nk, tq_pad, tk_pad;
   int causal;
+  int fuse_delta;  // bf16 dq computes D = rowsum(dO * O) itself and writes it
   float scale, scale_log2;
 };
 
@@ -720,7 +721,31 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     }
   }
   const size_t li = ((size_t)b * a.Hq + head) * a.T + min(qpos, a.T - 1);
-  const float lse_raw = a.lse[li], dlt_raw = a.delta[li];
+  const float lse_raw = a.lse[li];
+  float dlt_raw;
+  if (a.fuse_delta) {
+    // D = rowsum(dO * O): this lane holds half of the row's 64 dims
+    const bf16* os = reinterpret_cast<const bf16*>(a.out) +
+                     (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
+    float part = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4 ow = ld_u32x4(os + ks * 16);
+      const u32x4 gw = __builtin_bit_cast(u32x4, gf[ks]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // through scalars: __builtin_bit_cast of a vector element reads
+        // element 0 whatever the index (clang 22)
+        const uint32_t oj = ow[j], gj = gw[j];
+        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, oj),
+                                               __builtin_bit_cast(bf16x2, gj), part, false);
+      }
+    }
+    dlt_raw = halves_sum(part);
+    if (qvalid && half == 0) a.delta[li] = dlt_raw;
+  } else {
+    dlt_raw = a.delta[li];
+  }
   drain_memory();
   const float lse2 = qactive ? lse_raw * kLog2e : kPosInf;
   const float dlt = qactive ? dlt_raw : 0.f;
@@ -1158,7 +1183,11 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   a.scale_log2 = scale * kLog2e;
   const size_t rows = (size_t)batch * T * Hq;
   const unsigned dgrid = (unsigned)((rows + 255) / 256);
-  if (phases & 1) {
+  // bf16 with both the delta and the dq phase: the dq kernel, which holds
+  // the dO rows of its queries in registers anyway, also loads O and writes
+  // D; the separate delta pass (a full read of O and dO) is skipped
+  a.fuse_delta = !f32 && (phases & 3) == 3;
+  if ((phases & 1) && !a.fuse_delta) {
     if (f32)
       hipLaunchKernelGGL((bwd_delta_kernel<true>), dim3(dgrid), dim3(256), 0, stream, a, batch);
     else
