@@ -146,6 +146,22 @@ int mf_decode(const void* q, const void* k_cache, const void* v_cache,
               int q_heads, int kv_heads, int head_dim, float scale, void* out,
               void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode step with the ragged KV-cache append: writes row b's new key and
+ * value (k_new, v_new: [B, 1, Hkv, 64]) into slot
+ * clamp(positions[b], 0, capacity - 1) of k_cache / v_cache IN PLACE, then
+ * attends q over positions[b] + 1 slots with mf_decode's semantics (so a
+ * position at or past the capacity reads every slot, and a negative one gives
+ * the uniform average).  Replaces the scalar
+ * `dynamic_update_slice` + `cached_attention(valid_length=position + 1)` of
+ * layers/attention.py:309-317 (called from models/lfm2_5/decode.py:249-258)
+ * with one slot per row; the append runs in the decode's first launch, so a
+ * step costs no extra kernel.  Workspace as mf_decode. */
+int mf_decode_append(const void* q, const void* k_new, const void* v_new,
+                     const int32_t* positions, int dtype, int batch,
+                     int capacity, int q_heads, int kv_heads, int head_dim,
+                     float scale, void* k_cache, void* v_cache, void* out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* mf_last_error(void);
 

@@ -24,7 +24,8 @@ size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk);
 int decode_chunk(bool f32);
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
                          bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
-                         void* workspace, hipStream_t stream);
+                         void* workspace, hipStream_t stream, const void* k_new = nullptr,
+                         const void* v_new = nullptr, const int32_t* positions = nullptr);
 }  // namespace mf
 
 namespace {
@@ -217,6 +218,44 @@ size_t mf_decode_workspace_bytes(int batch, int capacity, int q_heads, int head_
   if (batch < 1 || capacity < 1 || q_heads < 1 || head_dim != mf::kD) return 0;
   // bf16 uses the smaller chunk count; size for the fp32 chunk (the larger one)
   return mf::decode_workspace_bytes(batch, capacity, q_heads, mf::decode_chunk(true));
+}
+
+namespace {
+
+int check_decode(int dtype, int batch, int capacity, int q_heads, int kv_heads, int head_dim,
+                 size_t workspace_bytes) {
+  if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
+  if (batch < 1 || capacity < 1 || q_heads < 1 || kv_heads < 1)
+    return fail(MF_ERR_INVALID_ARGUMENT,
+                "Sizes must be positive (batch=%d capacity=%d q_heads=%d kv_heads=%d)", batch,
+                capacity, q_heads, kv_heads);
+  if (head_dim != mf::kD)
+    return fail(MF_ERR_SHAPE, "Cached attention query/KV shapes are incompatible");
+  if (q_heads % kv_heads) return fail(MF_ERR_HEADS, "Query heads must be divisible by KV heads");
+  if (q_heads / kv_heads > 8)
+    return fail(MF_ERR_HEADS, "Decode serves at most 8 query heads per KV head (got %d)",
+                q_heads / kv_heads);
+  const size_t need = mf_decode_workspace_bytes(batch, capacity, q_heads, head_dim);
+  if (workspace_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  return MF_OK;
+}
+
+}  // namespace
+
+int mf_decode_append(const void* q, const void* k_new, const void* v_new,
+                     const int32_t* positions, int dtype, int batch, int capacity, int q_heads,
+                     int kv_heads, int head_dim, float scale, void* k_cache, void* v_cache,
+                     void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!q || !k_new || !v_new || !positions || !k_cache || !v_cache || !out || !workspace)
+    return fail(MF_ERR_INVALID_ARGUMENT, "every tensor pointer and the workspace must be non-null");
+  if (int rc = check_decode(dtype, batch, capacity, q_heads, kv_heads, head_dim, workspace_bytes))
+    return rc;
+  return check_hip(mf::launch_decode(q, k_cache, v_cache, nullptr, dtype == MF_DTYPE_F32, batch,
+                                     capacity, q_heads, kv_heads, scale, out, workspace,
+                                     static_cast<hipStream_t>(stream), k_new, v_new, positions),
+                   "mf_decode_append launch");
 }
 
 int mf_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* lengths,

@@ -25,6 +25,14 @@ struct DecArgs {
   const void* k;
   const void* v;
   const int32_t* lengths;
+  // decode-step append: the step's key/value rows and per-row cache slots;
+  // null for a plain decode
+  const void* k_new;
+  const void* v_new;
+  const int32_t* positions;
+  int32_t* step_lengths;  // positions + 1, the lengths the step attends over
+  void* k_cache;          // writable views of k / v for the append
+  void* v_cache;
   void* out;
   int* offsets;    // [B + 1] chunk offsets
   float* partial;  // [B][Hq][maxc][2 + D]: (scaled max, sum, acc[D])
@@ -40,7 +48,38 @@ __device__ __forceinline__ int eff_len(int len, int cap) {
   return len <= 0 ? cap : (len > cap ? cap : len);
 }
 
+// Decode-step append (dynamic_update_slice of one token per row): row b's
+// key/value go to slot clamp(positions[b], 0, cap - 1) -- the start index
+// clamping of dynamic_update_slice -- and the step attends over
+// positions[b] + 1 slots.  16-byte copies; the decode kernels of the same
+// stream read the cache after this kernel.
+template <int ELEM>
+__device__ void append_rows(const DecArgs& a) {
+  constexpr int kChunks = kD * ELEM / 16;  // 16-byte chunks per (row, head)
+  const int total = a.B * a.Hkv * kChunks;
+  for (int i = threadIdx.x; i < total; i += blockDim.x) {
+    const int ch = i % kChunks;
+    const int bh = i / kChunks;
+    const int b = bh / a.Hkv, h = bh % a.Hkv;
+    const int slot = min(max(a.positions[b], 0), a.cap - 1);
+    const size_t src = ((size_t)bh * kD) * ELEM + ch * 16;
+    const size_t dst = ((((size_t)b * a.cap + slot) * a.Hkv + h) * kD) * ELEM + ch * 16;
+    st_u32x4(reinterpret_cast<char*>(a.k_cache) + dst, ld_u32x4(reinterpret_cast<const char*>(a.k_new) + src));
+    st_u32x4(reinterpret_cast<char*>(a.v_cache) + dst, ld_u32x4(reinterpret_cast<const char*>(a.v_new) + src));
+  }
+}
+
+template <int ELEM>
 __global__ __launch_bounds__(256) void decode_prep_kernel(DecArgs a) {
+  if (a.positions) {
+    append_rows<ELEM>(a);
+    for (int b = threadIdx.x; b < a.B; b += blockDim.x) {
+      const long long len = (long long)a.positions[b] + 1;
+      a.step_lengths[b] = (int)min(max(len, (long long)INT32_MIN), (long long)INT32_MAX);
+    }
+    __syncthreads();
+    a.lengths = a.step_lengths;
+  }
   // Block-wide exclusive scan of per-row chunk counts (B may exceed 256).
   __shared__ int part[256];
   __shared__ int carry;
@@ -466,9 +505,10 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
   else reinterpret_cast<float*>(a.out)[(size_t)bh * kD + lane] = o;
 }
 
+// workspace: chunk offsets [B + 1], step lengths [B], partials
 size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk) {
   const int maxc = (cap + chunk - 1) / chunk;
-  return align256(sizeof(int) * (size_t)(batch + 1)) +
+  return align256(sizeof(int) * (size_t)(batch + 1)) + align256(sizeof(int) * (size_t)batch) +
          sizeof(float) * (size_t)batch * Hq * maxc * (2 + kD);
 }
 
@@ -476,12 +516,18 @@ int decode_chunk(bool f32) { return f32 ? 128 : kDecChunk; }
 
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
                          bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
-                         void* workspace, hipStream_t stream) {
+                         void* workspace, hipStream_t stream, const void* k_new,
+                         const void* v_new, const int32_t* positions) {
   DecArgs a;
   a.q = q;
   a.k = k;
   a.v = v;
   a.lengths = lengths;
+  a.k_new = k_new;
+  a.v_new = v_new;
+  a.positions = positions;
+  a.k_cache = const_cast<void*>(k);
+  a.v_cache = const_cast<void*>(v);
   a.out = out;
   a.B = batch;
   a.cap = cap;
@@ -493,8 +539,14 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
   a.scale_log2 = scale * kLog2e;
   char* ws = reinterpret_cast<char*>(workspace);
   a.offsets = reinterpret_cast<int*>(ws);
-  a.partial = reinterpret_cast<float*>(ws + align256(sizeof(int) * (size_t)(batch + 1)));
-  hipLaunchKernelGGL(decode_prep_kernel, dim3(1), dim3(256), 0, stream, a);
+  a.step_lengths = reinterpret_cast<int32_t*>(ws + align256(sizeof(int) * (size_t)(batch + 1)));
+  a.partial = reinterpret_cast<float*>(ws + align256(sizeof(int) * (size_t)(batch + 1)) +
+                                       align256(sizeof(int) * (size_t)batch));
+  if (f32)
+    hipLaunchKernelGGL((decode_prep_kernel<4>), dim3(1), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((decode_prep_kernel<2>), dim3(1), dim3(256), 0, stream, a);
+  if (positions) a.lengths = a.step_lengths;  // the kernels below attend over positions + 1
   const int upper = batch * a.maxc;
   int gx = (1024 + Hkv - 1) / Hkv;
   if (gx > upper) gx = upper;

@@ -47,6 +47,7 @@ EXPORTS = (
     "mf_attn_bwd_dkdv",
     "mf_decode_workspace_bytes",
     "mf_decode",
+    "mf_decode_append",
     "mf_last_error",
     "mf_version",
 )
@@ -101,6 +102,9 @@ def _load() -> ctypes.CDLL:
     lib.mf_decode_workspace_bytes.restype = sz
     lib.mf_decode.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, vp, vp, sz, vp]
     lib.mf_decode.restype = i32
+    lib.mf_decode_append.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, vp, vp, vp,
+                                     vp, sz, vp]
+    lib.mf_decode_append.restype = i32
     lib.mf_last_error.argtypes = []
     lib.mf_last_error.restype = ctypes.c_char_p
     lib.mf_version.argtypes = []

@@ -133,3 +133,50 @@ def cached_attention(
     except KeyError:
         raise ValueError(f"Unsupported cached attention backend: {backend}") from None
     return fn(query, key, value, valid_length)
+
+
+def cached_attention_step(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    cache_key: torch.Tensor,
+    cache_value: torch.Tensor,
+    position,
+    *,
+    backend: str = "cudnn",
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """One decode step's cache write and attention, per row.
+
+    The attention part of ``attention_block_step``
+    (``layers/attention.py:309-317``): ``key``/``value`` ``[B, 1, Hkv, D]``
+    are written at cache slot ``position`` -- a scalar, as in the reference,
+    or one slot per row -- with ``dynamic_update_slice``'s clamping of the
+    start index to ``[0, capacity - 1]``, and the query attends over
+    ``position + 1`` slots.  The caches are updated in place and returned, so
+    callers that rebind them (``cache_key = ...``) keep working.
+    """
+    if backend not in _CACHED_BACKENDS:
+        raise ValueError(f"Unsupported cached attention backend: {backend}")
+    if (query.shape[-1] != cache_key.shape[-1] or cache_key.shape != cache_value.shape
+            or key.shape != value.shape or key.shape[1] != 1 or query.shape[1] != 1
+            or key.shape[0] != cache_key.shape[0] or key.shape[2:] != cache_key.shape[2:]):
+        raise ValueError("Cached attention query/KV shapes are incompatible")
+    if query.shape[2] % cache_key.shape[2]:
+        raise ValueError("Query heads must be divisible by KV heads")
+    if query.shape[-1] != _lib.HEAD_DIM:
+        # padded head dims: append through the padded copies, then write back
+        (q, kn, vn, kc, vc), d = fit_head_dim(query.contiguous(), key.contiguous(),
+                                              value.contiguous(), cache_key.contiguous(),
+                                              cache_value.contiguous())
+        out = ops.decode_append(q, kn, vn, kc, vc, _lengths(position, query.shape[0],
+                                                              query.device), d ** -0.5)
+        cache_key.copy_(kc[..., :d])
+        cache_value.copy_(vc[..., :d])
+        return out[..., :d], cache_key, cache_value
+    for t in (cache_key, cache_value):
+        if not t.is_contiguous():
+            raise ValueError("the KV caches must be contiguous to be updated in place")
+    positions = _lengths(position, query.shape[0], query.device)
+    out = ops.decode_append(query.contiguous(), key.contiguous(), value.contiguous(), cache_key,
+                            cache_value, positions, query.shape[-1] ** -0.5)
+    return out, cache_key, cache_value

@@ -164,6 +164,24 @@ def attn_bwd_dkdv(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, d
                                          ws.numel(), _stream(q.device)))
 
 
+def decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                  k_cache: torch.Tensor, v_cache: torch.Tensor, positions: torch.Tensor,
+                  scale: float) -> torch.Tensor:
+    """Write each row's new key/value into its cache slot (in place), then decode."""
+    device = require_device(q, k_new, v_new, k_cache, v_cache, positions)
+    code = dtype_code(q)
+    b, _, hq, d = q.shape
+    cap, hkv = k_cache.shape[1], k_cache.shape[2]
+    out = torch.empty_like(q)
+    ws_bytes = _lib.LIB.mf_decode_workspace_bytes(b, cap, hq, d)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    _lib.check(_lib.LIB.mf_decode_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(positions), code,
+                                         b, cap, hq, hkv, d, float(scale), _ptr(k_cache),
+                                         _ptr(v_cache), _ptr(out), _ptr(ws), ws_bytes,
+                                         _stream(device)))
+    return out
+
+
 def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
            lengths: torch.Tensor, scale: float) -> torch.Tensor:
     device = require_device(q, k_cache, v_cache, lengths)

@@ -96,6 +96,20 @@ def test_block_map_and_decode_reject_bad_arguments():
     assert L.mf_decode_workspace_bytes(64, 8192, 16, 64) > 0
 
 
+def test_decode_append_rejects_bad_arguments():
+    L = _lib.LIB
+    args = [None] * 4 + [1, 2, 6, 4, 2, 64, 1.0] + [None] * 4 + [0, None]
+    assert L.mf_decode_append(*args) == _lib.ERR_INVALID_ARGUMENT
+    buf = ctypes.c_char_p(b"x")  # any non-null host address: validation fails before any launch
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    full = [p] * 4 + [1, 2, 6, 4, 2, 64, 1.0] + [p] * 4 + [0, None]
+    assert L.mf_decode_append(*full) == _lib.ERR_WORKSPACE
+    full[9] = 8
+    assert L.mf_decode_append(*full) == _lib.ERR_SHAPE
+    full[9], full[7] = 64, 3
+    assert L.mf_decode_append(*full) == _lib.ERR_HEADS
+
+
 def test_error_codes_map_to_value_errors():
     rc = _fwd(hq=3)
     with pytest.raises(ValueError, match="divisible"):

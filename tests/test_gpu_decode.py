@@ -91,3 +91,54 @@ def test_scalar_length_broadcasts_and_backends_agree(device):
     a = attention.cached_attention(q, k, k, 17, backend="dense")
     b = attention.cached_attention(q, k, k, torch.full((3,), 17, dtype=torch.int32), backend="cudnn")
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_step_appends_per_row(dtype, device):
+    """Ragged KV-cache append + decode (layers/attention.py:309-317, one slot per row).
+
+    Slots follow dynamic_update_slice's start clamping to [0, capacity - 1];
+    the step attends over position + 1 slots (position >= capacity reads every
+    slot, a negative position gives the uniform average, as mf_decode)."""
+    rng = np.random.default_rng(9)
+    cap, hq, hkv = 300, 8, 2
+    positions = np.array([0, 1, 150, 255, 256, 299, 300, 1000, -1], np.int32)
+    b = positions.size
+    say("decode append", dtype, positions.tolist())
+    t = lambda x: torch.tensor(x, device=device).to(dtype)  # noqa: E731
+    q, kn, vn = (t(rng.standard_normal(s).astype(np.float32))
+                 for s in ((b, 1, hq, 64), (b, 1, hkv, 64), (b, 1, hkv, 64)))
+    kc, vc = (t(rng.standard_normal((b, cap, hkv, 64)).astype(np.float32)) for _ in range(2))
+    ekc, evc = kc.clone(), vc.clone()
+    slots = np.clip(positions, 0, cap - 1)
+    for i in range(b):
+        ekc[i, slots[i]] = kn[i, 0]
+        evc[i, slots[i]] = vn[i, 0]
+    out, kc2, vc2 = attention.cached_attention_step(q, kn, vn, kc, vc,
+                                                     torch.tensor(positions, device=device))
+    assert kc2 is kc and vc2 is vc
+    assert torch.equal(kc, ekc) and torch.equal(vc, evc)
+    # same kernels as a plain decode over the written caches: bit-identical
+    plain = attention.dense_cached_attention(q, ekc, evc, torch.tensor(positions + 1, device=device))
+    assert torch.equal(out, plain)
+    ref = oatt.cached_fp64(q.float().cpu().numpy(), ekc.float().cpu().numpy(),
+                           evc.float().cpu().numpy(), positions + 1)[0]
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, rtol=tol, atol=tol)
+
+
+def test_decode_step_scalar_position_and_small_head_dim(device):
+    rng = np.random.default_rng(10)
+    say("decode append scalar / D=8")
+    b, cap, hq, hkv, d = 3, 12, 4, 2, 8
+    t = lambda x: torch.tensor(x, dtype=torch.float32, device=device)  # noqa: E731
+    q, kn, vn = (t(rng.standard_normal(s)) for s in ((b, 1, hq, d), (b, 1, hkv, d), (b, 1, hkv, d)))
+    kc, vc = (t(rng.standard_normal((b, cap, hkv, d))) for _ in range(2))
+    k0, v0 = kc.clone(), vc.clone()
+    out, kc2, vc2 = attention.cached_attention_step(q, kn, vn, kc, vc, 5)
+    k0[:, 5], v0[:, 5] = kn[:, 0], vn[:, 0]
+    assert torch.equal(kc2, k0) and torch.equal(vc2, v0)
+    ref = oatt.cached_fp64(q.cpu().numpy(), k0.cpu().numpy(), v0.cpu().numpy(), np.full(b, 6))[0]
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    with pytest.raises(ValueError, match="Unsupported cached attention backend"):
+        attention.cached_attention_step(q, kn, vn, kc, vc, 5, backend="splash")
