@@ -162,6 +162,26 @@ int mf_decode_append(const void* q, const void* k_new, const void* v_new,
                      float scale, void* k_cache, void* v_cache, void* out,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* Attention prologue: RMS-normalise every q and k head over its 64 dims with
+ * per-dimension gains (q_gain, k_gain: [64] in the tensor dtype), then apply
+ * rotary embeddings at per-token positions ([B, T] int32; NULL means
+ * 0 .. T-1 on every row), in one pass.  Replaces the two rms_norm and two
+ * apply_rotary calls of layers/attention.py:62-97 (kernels/normalization.py:7-22,
+ * kernels/rotary.py:7-39) on the packed path, where positions restart at
+ * every segment (layers/attention.py:224-227).  q_out / k_out may alias q /
+ * k.  Layout [B, T, H, 64]; eps and rope_theta as the reference's. */
+int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain,
+                    const void* k_gain, const int32_t* positions, int dtype,
+                    int batch, int seq_len, int q_heads, int kv_heads,
+                    int head_dim, float eps, float rope_theta, void* q_out,
+                    void* k_out, void* stream);
+
+/* Per-token positions from segment ids on the device: the offset of each
+ * token inside its run of equal nonzero ids, 0 for padding -- the positions
+ * batching/packing.py:92-100 builds on the host for packed rows. */
+int mf_segment_positions(const int32_t* segment_ids, int batch, int seq_len,
+                         int32_t* positions, void* stream);
+
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* mf_last_error(void);
 

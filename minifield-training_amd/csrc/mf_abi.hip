@@ -26,6 +26,12 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
                          bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
                          void* workspace, hipStream_t stream, const void* k_new = nullptr,
                          const void* v_new = nullptr, const int32_t* positions = nullptr);
+hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* q_gain,
+                               const void* k_gain, const int32_t* positions, bool f32, int B,
+                               int T, int Hq, int Hkv, float eps, float theta, void* q_out,
+                               void* k_out, hipStream_t stream);
+hipError_t launch_segment_positions(const int32_t* seg, int B, int T, int32_t* pos,
+                                    hipStream_t stream);
 }  // namespace mf
 
 namespace {
@@ -282,6 +288,39 @@ int mf_decode(const void* q, const void* k_cache, const void* v_cache, const int
                                      capacity, q_heads, kv_heads, scale, out, workspace,
                                      static_cast<hipStream_t>(stream)),
                    "mf_decode launch");
+}
+
+int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain, const void* k_gain,
+                    const int32_t* positions, int dtype, int batch, int seq_len, int q_heads,
+                    int kv_heads, int head_dim, float eps, float rope_theta, void* q_out,
+                    void* k_out, void* stream) {
+  if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
+  if (batch < 1 || seq_len < 1 || q_heads < 1 || kv_heads < 1)
+    return fail(MF_ERR_INVALID_ARGUMENT,
+                "Sizes must be positive (batch=%d seq_len=%d q_heads=%d kv_heads=%d)", batch,
+                seq_len, q_heads, kv_heads);
+  if (head_dim != mf::kD)
+    return fail(MF_ERR_HEAD_DIM, "head_dim must be %d (got %d)", mf::kD, head_dim);
+  if (!q || !k || !q_gain || !k_gain || !q_out || !k_out)
+    return fail(MF_ERR_INVALID_ARGUMENT, "a required tensor pointer is null");
+  if (!(rope_theta > 0.f)) return fail(MF_ERR_INVALID_ARGUMENT, "rope_theta must be positive");
+  return check_hip(mf::launch_qk_norm_rope(q, k, q_gain, k_gain, positions, dtype == MF_DTYPE_F32,
+                                           batch, seq_len, q_heads, kv_heads, eps, rope_theta,
+                                           q_out, k_out, static_cast<hipStream_t>(stream)),
+                   "mf_qk_norm_rope launch");
+}
+
+int mf_segment_positions(const int32_t* segment_ids, int batch, int seq_len, int32_t* positions,
+                         void* stream) {
+  if (batch < 1 || seq_len < 1)
+    return fail(MF_ERR_INVALID_ARGUMENT, "Sizes must be positive (batch=%d seq_len=%d)", batch,
+                seq_len);
+  if (!segment_ids || !positions)
+    return fail(MF_ERR_INVALID_ARGUMENT, "segment_ids and positions must be non-null");
+  return check_hip(mf::launch_segment_positions(segment_ids, batch, seq_len, positions,
+                                                static_cast<hipStream_t>(stream)),
+                   "mf_segment_positions launch");
 }
 
 const char* mf_last_error(void) { return g_last_error.c_str(); }

@@ -687,7 +687,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
 // transposing LDS reads.
 // ---------------------------------------------------------------------------
 template <int HPW>
-__global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2 * HPW)))
 void bwd_dq_bf16_kernel(BwdArgs a) {
   constexpr int W = 4 * HPW;
   __shared__ __attribute__((aligned(16))) char stage0[kStageBytes], stage1[kStageBytes],

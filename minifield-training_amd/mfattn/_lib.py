@@ -48,6 +48,8 @@ EXPORTS = (
     "mf_decode_workspace_bytes",
     "mf_decode",
     "mf_decode_append",
+    "mf_qk_norm_rope",
+    "mf_segment_positions",
     "mf_last_error",
     "mf_version",
 )
@@ -105,6 +107,11 @@ def _load() -> ctypes.CDLL:
     lib.mf_decode_append.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, vp, vp, vp,
                                      vp, sz, vp]
     lib.mf_decode_append.restype = i32
+    lib.mf_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, f32,
+                                    vp, vp, vp]
+    lib.mf_qk_norm_rope.restype = i32
+    lib.mf_segment_positions.argtypes = [vp, i32, i32, vp, vp]
+    lib.mf_segment_positions.restype = i32
     lib.mf_last_error.argtypes = []
     lib.mf_last_error.restype = ctypes.c_char_p
     lib.mf_version.argtypes = []
