@@ -182,6 +182,23 @@ int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain,
 int mf_segment_positions(const int32_t* segment_ids, int batch, int seq_len,
                          int32_t* positions, void* stream);
 
+/* Segmented short (depthwise) convolution of the packed conv layers, gates
+ * fused:  out = c_gate * conv(b_gate * values)  over [B, T, C] (C a multiple
+ * of 8), taps [C, kernel_size] (kernel_size <= 8) in the tensor dtype.  A tap
+ * at token s contributes to token t only when 0 <= s < T and, with segment
+ * ids, segment_ids[s] == segment_ids[t] != 0 -- segment boundaries act as the
+ * zero padding of an independently processed sequence.
+ *   MF_CONV_CAUSAL:   taps at t-(K-1) .. t  (kernels/convolution.py:25-53)
+ *   MF_CONV_CENTERED: taps at t-K/2 .. t+K-1-K/2 (kernels/bidirectional.py:38-58,
+ *                     as models/lfm2_5/encoder.py:80-85 calls it)
+ * b_gate, c_gate and segment_ids may be NULL (no gate / no segments). */
+#define MF_CONV_CAUSAL 0
+#define MF_CONV_CENTERED 1
+int mf_segmented_conv(const void* b_gate, const void* c_gate, const void* values,
+                      const void* taps, const int32_t* segment_ids, int mode,
+                      int dtype, int batch, int seq_len, int channels,
+                      int kernel_size, void* out, void* stream);
+
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* mf_last_error(void);
 

@@ -32,6 +32,9 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* q_gain,
                                void* k_out, hipStream_t stream);
 hipError_t launch_segment_positions(const int32_t* seg, int B, int T, int32_t* pos,
                                     hipStream_t stream);
+hipError_t launch_segmented_conv(const void* b, const void* c, const void* v, const void* w,
+                                 const int32_t* seg, bool centered, bool f32, int B, int T, int C,
+                                 int K, void* out, hipStream_t stream);
 }  // namespace mf
 
 namespace {
@@ -321,6 +324,30 @@ int mf_segment_positions(const int32_t* segment_ids, int batch, int seq_len, int
   return check_hip(mf::launch_segment_positions(segment_ids, batch, seq_len, positions,
                                                 static_cast<hipStream_t>(stream)),
                    "mf_segment_positions launch");
+}
+
+int mf_segmented_conv(const void* b_gate, const void* c_gate, const void* values,
+                      const void* taps, const int32_t* segment_ids, int mode, int dtype,
+                      int batch, int seq_len, int channels, int kernel_size, void* out,
+                      void* stream) {
+  if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
+  if (mode != MF_CONV_CAUSAL && mode != MF_CONV_CENTERED)
+    return fail(MF_ERR_MODE, "Unsupported convolution mode %d", mode);
+  if (batch < 1 || seq_len < 1 || channels < 1)
+    return fail(MF_ERR_INVALID_ARGUMENT, "Sizes must be positive (batch=%d seq_len=%d channels=%d)",
+                batch, seq_len, channels);
+  if (channels % 8)
+    return fail(MF_ERR_SHAPE, "channels must be a multiple of 8 (got %d)", channels);
+  if (kernel_size < 1 || kernel_size > 8)
+    return fail(MF_ERR_SHAPE, "kernel_size must be in [1, 8] (got %d)", kernel_size);
+  if (!values || !taps || !out)
+    return fail(MF_ERR_INVALID_ARGUMENT, "values, taps and out must be non-null");
+  return check_hip(mf::launch_segmented_conv(b_gate, c_gate, values, taps, segment_ids,
+                                             mode == MF_CONV_CENTERED, dtype == MF_DTYPE_F32,
+                                             batch, seq_len, channels, kernel_size, out,
+                                             static_cast<hipStream_t>(stream)),
+                   "mf_segmented_conv launch");
 }
 
 const char* mf_last_error(void) { return g_last_error.c_str(); }

@@ -32,6 +32,9 @@ MODE_PACKED_CAUSAL = 0
 MODE_PACKED_BIDIR = 1
 MODE_KEYMASK_BIDIR = 2
 
+CONV_CAUSAL = 0
+CONV_CENTERED = 1
+
 TILE = 128
 HEAD_DIM = 64
 
@@ -50,6 +53,7 @@ EXPORTS = (
     "mf_decode_append",
     "mf_qk_norm_rope",
     "mf_segment_positions",
+    "mf_segmented_conv",
     "mf_last_error",
     "mf_version",
 )
@@ -112,6 +116,8 @@ def _load() -> ctypes.CDLL:
     lib.mf_qk_norm_rope.restype = i32
     lib.mf_segment_positions.argtypes = [vp, i32, i32, vp, vp]
     lib.mf_segment_positions.restype = i32
+    lib.mf_segmented_conv.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
+    lib.mf_segmented_conv.restype = i32
     lib.mf_last_error.argtypes = []
     lib.mf_last_error.restype = ctypes.c_char_p
     lib.mf_version.argtypes = []
