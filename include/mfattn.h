@@ -86,6 +86,18 @@ int mf_block_map(const int32_t* segment_ids, const void* mask, int mask_dtype,
                  int mode, int batch, int q_len, int kv_len, void* plan,
                  size_t plan_bytes, void* stream);
 
+/* The block map built from the packer's placements instead of [B, T] id and
+ * mask arrays: `placements` is [count][3] int32 (row, start, length), the
+ * i-th placed sequence getting segment id i + 1 and positions
+ * 0 .. length-1 -- the PackedRows of batching/packing.py:74-102, whose
+ * attention mask is segment_ids != 0.  Placements must not overlap (the
+ * packer's guarantee).  Optionally also writes the [B, length] segment ids
+ * and positions (either pointer may be NULL).  Modes MF_MODE_PACKED_*. */
+int mf_block_map_placements(const int32_t* placements, int count, int mode,
+                            int batch, int length, void* plan,
+                            size_t plan_bytes, int32_t* segment_ids_out,
+                            int32_t* positions_out, void* stream);
+
 /* Forward.  Replaces _dense_attention with its callers
  * dense_packed_causal_attention (kernels/attention.py:245-261, mode 0) and
  * bidirectional.attention (kernels/bidirectional.py:7-35, modes 1 and 2).

@@ -32,6 +32,9 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* q_gain,
                                void* k_out, hipStream_t stream);
 hipError_t launch_segment_positions(const int32_t* seg, int B, int T, int32_t* pos,
                                     hipStream_t stream);
+hipError_t launch_block_map_placements(const int32_t* placements, int count, int mode, int batch,
+                                       int length, void* plan, int32_t* seg_out, int32_t* pos_out,
+                                       hipStream_t stream);
 hipError_t launch_segmented_conv(const void* b, const void* c, const void* v, const void* w,
                                  const int32_t* seg, bool centered, bool f32, int B, int T, int C,
                                  int K, void* out, hipStream_t stream);
@@ -133,6 +136,26 @@ int mf_block_map(const int32_t* segment_ids, const void* mask, int mask_dtype, i
   return check_hip(mf::launch_block_map(segment_ids, mask, mask_dtype == MF_MASK_U8, mode, batch,
                                         q_len, kv_len, plan, static_cast<hipStream_t>(stream)),
                    "mf_block_map launch");
+}
+
+int mf_block_map_placements(const int32_t* placements, int count, int mode, int batch,
+                            int length, void* plan, size_t plan_bytes, int32_t* segment_ids_out,
+                            int32_t* positions_out, void* stream) {
+  if (mode != MF_MODE_PACKED_CAUSAL && mode != MF_MODE_PACKED_BIDIR)
+    return fail(MF_ERR_MODE, "placements describe packed rows (mode %d or %d), got %d",
+                MF_MODE_PACKED_CAUSAL, MF_MODE_PACKED_BIDIR, mode);
+  if (batch < 1 || length < 1 || count < 0)
+    return fail(MF_ERR_INVALID_ARGUMENT, "Sizes must be positive (batch=%d length=%d count=%d)",
+                batch, length, count);
+  if ((count > 0 && !placements) || !plan)
+    return fail(MF_ERR_INVALID_ARGUMENT, "placements and plan must be non-null");
+  const size_t need = mf::plan_layout(batch, length, length).total;
+  if (plan_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "plan holds %zu bytes, %zu needed", plan_bytes, need);
+  return check_hip(mf::launch_block_map_placements(placements, count, mode, batch, length, plan,
+                                                   segment_ids_out, positions_out,
+                                                   static_cast<hipStream_t>(stream)),
+                   "mf_block_map_placements launch");
 }
 
 int mf_attn_fwd(const void* q, const void* k, const void* v, int dtype, int batch, int q_len,

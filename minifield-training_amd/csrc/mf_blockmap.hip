@@ -231,6 +231,68 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(MapArgs a) {
   for (int i = lo; i < hi; ++i) order[hist[order_bucket(len[i])][t]++] = i;
 }
 
+// Canonical ids straight from the packer's placements (row, start, length)
+// -- batching/packing.py:74-102 gives the i-th placed sequence segment id
+// i + 1 and positions arange(length) -- so no [B, T] id array has to be
+// built on the host and copied in.  Two passes: clear, then one block per
+// placement writes its tokens (placements do not overlap, as the packer
+// guarantees; tokens outside [0, T) are dropped).
+__global__ __launch_bounds__(256) void placement_clear_kernel(MapArgs a, int32_t* seg_out,
+                                                              int32_t* pos_out) {
+  const int b = blockIdx.y;
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p < a.lay.tq_pad) plan_i32(a.plan, a.lay.qid)[(size_t)b * a.lay.tq_pad + p] = 0;
+  if (p < a.lay.tk_pad) plan_i32(a.plan, a.lay.kid)[(size_t)b * a.lay.tk_pad + p] = 0;
+  if (p < a.q_len) {
+    if (seg_out) seg_out[(size_t)b * a.q_len + p] = 0;
+    if (pos_out) pos_out[(size_t)b * a.q_len + p] = 0;
+  }
+}
+
+__global__ __launch_bounds__(256) void placement_ids_kernel(MapArgs a, const int32_t* placements,
+                                                            int32_t* seg_out, int32_t* pos_out) {
+  const int i = blockIdx.x;
+  const int row = placements[3 * i], start = placements[3 * i + 1], len = placements[3 * i + 2];
+  if (row < 0 || row >= a.batch) return;
+  const int lo = max(start, 0), hi = min(start + len, a.q_len);
+  for (int t = lo + threadIdx.x; t < hi; t += blockDim.x) {
+    plan_i32(a.plan, a.lay.qid)[(size_t)row * a.lay.tq_pad + t] = i + 1;
+    plan_i32(a.plan, a.lay.kid)[(size_t)row * a.lay.tk_pad + t] = i + 1;
+    if (seg_out) seg_out[(size_t)row * a.q_len + t] = i + 1;
+    if (pos_out) pos_out[(size_t)row * a.q_len + t] = t - start;
+  }
+}
+
+static void launch_map_tail(const MapArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(tile_runs_kernel, dim3(a.lay.nq + a.lay.nk, a.batch), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL(classify_kernel, dim3((a.lay.nq * a.lay.nk + 255) / 256, a.batch), dim3(256),
+                     0, stream, a);
+  hipLaunchKernelGGL(worklist_kernel, dim3(a.lay.nq + a.lay.nk, a.batch), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL(order_kernel, dim3(2), dim3(kOrderThreads), 0, stream, a);
+}
+
+hipError_t launch_block_map_placements(const int32_t* placements, int count, int mode, int batch,
+                                       int length, void* plan, int32_t* seg_out, int32_t* pos_out,
+                                       hipStream_t stream) {
+  MapArgs a;
+  a.seg = nullptr;
+  a.mask = nullptr;
+  a.mask_u8 = 0;
+  a.mode = mode;
+  a.batch = batch;
+  a.q_len = length;
+  a.kv_len = length;
+  a.lay = plan_layout(batch, length, length);
+  a.plan = reinterpret_cast<char*>(plan);
+  hipLaunchKernelGGL(placement_clear_kernel, dim3((a.lay.tq_pad + 255) / 256, batch), dim3(256), 0,
+                     stream, a, seg_out, pos_out);
+  if (count > 0)
+    hipLaunchKernelGGL(placement_ids_kernel, dim3(count), dim3(256), 0, stream, a, placements,
+                       seg_out, pos_out);
+  launch_map_tail(a, stream);
+  return hipGetLastError();
+}
+
 hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, int mode,
                             int batch, int q_len, int kv_len, void* plan,
                             hipStream_t stream) {
@@ -246,11 +308,7 @@ hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, i
   a.plan = reinterpret_cast<char*>(plan);
   const int pad = a.lay.tq_pad > a.lay.tk_pad ? a.lay.tq_pad : a.lay.tk_pad;
   hipLaunchKernelGGL(token_ids_kernel, dim3((pad + 255) / 256, batch), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL(tile_runs_kernel, dim3(a.lay.nq + a.lay.nk, batch), dim3(64), 0, stream, a);
-  hipLaunchKernelGGL(classify_kernel, dim3((a.lay.nq * a.lay.nk + 255) / 256, batch), dim3(256),
-                     0, stream, a);
-  hipLaunchKernelGGL(worklist_kernel, dim3(a.lay.nq + a.lay.nk, batch), dim3(64), 0, stream, a);
-  hipLaunchKernelGGL(order_kernel, dim3(2), dim3(kOrderThreads), 0, stream, a);
+  launch_map_tail(a, stream);
   return hipGetLastError();
 }
 

@@ -42,6 +42,7 @@ EXPORTS = (
     "mf_plan_layout",
     "mf_plan_bytes",
     "mf_block_map",
+    "mf_block_map_placements",
     "mf_attn_fwd",
     "mf_attn_bwd_workspace_bytes",
     "mf_attn_bwd",
@@ -116,6 +117,8 @@ def _load() -> ctypes.CDLL:
     lib.mf_qk_norm_rope.restype = i32
     lib.mf_segment_positions.argtypes = [vp, i32, i32, vp, vp]
     lib.mf_segment_positions.restype = i32
+    lib.mf_block_map_placements.argtypes = [vp, i32, i32, i32, i32, vp, sz, vp, vp, vp]
+    lib.mf_block_map_placements.restype = i32
     lib.mf_segmented_conv.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
     lib.mf_segmented_conv.restype = i32
     lib.mf_last_error.argtypes = []

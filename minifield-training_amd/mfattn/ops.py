@@ -98,6 +98,25 @@ def block_map(segment_ids: torch.Tensor | None, mask: torch.Tensor, mode: int,
     return Plan(buf, batch, q_len, kv_len, mode)
 
 
+def block_map_from_placements(placements: torch.Tensor, mode: int, batch: int,
+                              length: int) -> tuple[Plan, torch.Tensor, torch.Tensor]:
+    """Plan, segment ids and positions from packer placements ``[N, 3]`` (row, start, len)."""
+    device = require_device(placements)
+    pl = placements.to(torch.int32).contiguous()
+    if pl.dim() != 2 or pl.shape[1] != 3:
+        raise ValueError("placements must be [count, 3] (row, start, length)")
+    nbytes = _lib.LIB.mf_plan_bytes(batch, length, length)
+    if nbytes == 0:
+        raise ValueError("Sizes must be positive")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    seg = torch.empty((batch, length), dtype=torch.int32, device=device)
+    pos = torch.empty_like(seg)
+    _lib.check(_lib.LIB.mf_block_map_placements(_ptr(pl), pl.shape[0], mode, batch, length,
+                                                _ptr(buf), nbytes, _ptr(seg), _ptr(pos),
+                                                _stream(device)))
+    return Plan(buf, batch, length, length, mode), seg, pos
+
+
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: Plan, mode: int,
              scale: float) -> tuple[torch.Tensor, torch.Tensor]:
     device = require_device(q, k, v)

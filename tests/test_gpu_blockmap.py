@@ -111,3 +111,33 @@ def test_bool_mask_dtype(device):
     seg = torch.tensor(w.segment_ids, device=device)
     a = ops.block_map(seg, mask, 0, w.length, w.length).tile_map().cpu().numpy()
     np.testing.assert_array_equal(a, masks.tile_map(0, w.attention_mask, w.segment_ids, 128, 128))
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_placements_build_the_same_plan(mode, device):
+    """mf_block_map_placements == mf_block_map over the packer's PackedRows."""
+    rng = np.random.default_rng(50 + mode)
+    for length in (256, 1000):
+        seqs = [list(range(int(n))) for n in rng.integers(1, min(300, length) + 1, size=9)]
+        rows = packing.rows_required([len(s) for s in seqs], length)
+        packed = packing.pack(seqs, rows, length, pad_token_id=0)
+        say("placements", mode, length, rows)
+        pl = torch.tensor([[p.row, p.start, p.length] for p in packed.placements], device=device)
+        plan, seg, pos = ops.block_map_from_placements(pl, mode, rows, length)
+        np.testing.assert_array_equal(seg.cpu().numpy(), packed.segment_ids)
+        np.testing.assert_array_equal(pos.cpu().numpy(), packed.positions)
+        mask = (packed.segment_ids != 0).astype(np.int32)
+        ref = ops.block_map(torch.tensor(packed.segment_ids, device=device),
+                            torch.tensor(mask, device=device), mode, length, length)
+        nq = nk = -(-length // 128)
+        for sec, dt, shape in ((0, torch.int32, (rows, nq * 128)), (1, torch.int32, (rows, nk * 128)),
+                               (2, torch.uint8, (rows, nq, nk)), (3, torch.int32, (rows, nq)),
+                               (5, torch.int32, (rows, nk)), (7, torch.int32, (rows * nq,)),
+                               (8, torch.int32, (rows * nk,))):
+            assert torch.equal(plan.section(sec, dt, shape), ref.section(sec, dt, shape)), sec
+        cnt = ref.section(3, torch.int32, (rows, nq)).cpu().numpy()
+        a, r = plan.section(4, torch.int32, (rows, nq, nk)).cpu().numpy(), \
+            ref.section(4, torch.int32, (rows, nq, nk)).cpu().numpy()
+        for row in range(rows):
+            for qi in range(nq):
+                np.testing.assert_array_equal(a[row, qi, : cnt[row, qi]], r[row, qi, : cnt[row, qi]])
