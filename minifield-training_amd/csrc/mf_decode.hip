@@ -48,6 +48,16 @@ __device__ __forceinline__ int eff_len(int len, int cap) {
   return len <= 0 ? cap : (len > cap ? cap : len);
 }
 
+// Row b's length as given: lengths[b], or positions[b] + 1 for a decode step
+// with an append (saturated to int32).
+__device__ __forceinline__ int raw_length(const int32_t* lengths, const int32_t* positions, int b) {
+  if (positions) {
+    const long long len = (long long)positions[b] + 1;
+    return (int)(len > INT32_MAX ? INT32_MAX : len);
+  }
+  return lengths[b];
+}
+
 // Decode-step append (dynamic_update_slice of one token per row): row b's
 // key/value go to slot clamp(positions[b], 0, cap - 1) -- the start index
 // clamping of dynamic_update_slice -- and the step attends over
@@ -348,41 +358,78 @@ __device__ __forceinline__ float across_groups(float x) {
 
 constexpr int kDecChunk = 256;  // tokens per work item (bf16)
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_prefix(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// Chunk count of the rows base + lane (0 past the batch).
+__device__ __forceinline__ int row_chunks(const DecArgs& a, int base) {
+  const int r = base + (threadIdx.x & 63);
+  return r < a.B ? (eff_len(raw_length(a.lengths, a.positions, r), a.cap) + kDecChunk - 1) / kDecChunk
+                 : 0;
+}
+
 template <int G>
-__global__ __launch_bounds__(256) void decode_bf16_kernel(DecArgs a) {
+__global__ __launch_bounds__(512) void decode_bf16_kernel(DecArgs a) {
   const int lane = threadIdx.x & 63;
   const int kg = lane >> 3, dl = lane & 7;
-  const int total = ld_const(a.offsets, a.B) * a.Hkv;
-  const int nwaves = gridDim.x * 4;
+  const int wpb = blockDim.x >> 6;  // waves per block
+  const int nwaves = gridDim.x * wpb;
   const float c = a.scale_log2;
   const float tau = 8.f / c;
   const bf16* ks = reinterpret_cast<const bf16*>(a.k);
   const bf16* vs = reinterpret_cast<const bf16*>(a.v);
+  // The (row, chunk) list is walked without a prefix-sum launch: every wave
+  // scans the rows' chunk counts itself (one 64-row block per step).
+  int total_chunks = 0;
+  for (int base = 0; base < a.B; base += 64) total_chunks += __shfl(wave_prefix(row_chunks(a, base)), 63);
+  const int total = uniform(total_chunks) * a.Hkv;
 
-  for (int item = uniform(blockIdx.x * 4 + (threadIdx.x >> 6)); item < total; item += nwaves) {
+  for (int item = uniform(blockIdx.x * wpb + (threadIdx.x >> 6)); item < total; item += nwaves) {
     const int kvh = item % a.Hkv;
     const int ci = item / a.Hkv;  // chunk item over all rows
-    int lo = 0, hi = a.B - 1;     // row: last b with offsets[b] <= ci
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (ld_const(a.offsets, mid) <= ci) lo = mid; else hi = mid - 1;
+    int b = 0, first = 0;         // row of chunk item ci and its first item
+    for (int base = 0, carry = 0; base < a.B; base += 64) {
+      const int incl = wave_prefix(row_chunks(a, base));
+      const int tot = __shfl(incl, 63);
+      if (ci < carry + tot) {
+        const int k = __popcll(__ballot(carry + incl <= ci));  // rows of the block before ci's
+        b = base + k;
+        first = carry + (k > 0 ? __shfl(incl, k - 1) : 0);
+        break;
+      }
+      carry += tot;
     }
-    const int b = uniform(lo);
-    const int chunk = ci - ld_const(a.offsets, b);
-    const int raw = ld_const(a.lengths, b);
+    b = uniform(b);
+    const int chunk = uniform(ci - first);
+    const int raw = uniform(raw_length(a.lengths, a.positions, b));
     const bool flat = raw <= 0;  // every slot masked: uniform weights
     const int len = eff_len(raw, a.cap);
     const int t0 = chunk * kDecChunk;
     const int n = min(kDecChunk, len - t0);
     const int last = t0 + n - 1;
+    // decode step with an append: slot `slot` reads the new row, and the
+    // wave whose chunk holds it writes that row to the cache (no other wave
+    // reads the slot)
+    const int slot = a.positions ? uniform(min(max(a.positions[b], 0), a.cap - 1)) : -1;
 
     u32x4 qv[G];
 #pragma unroll
     for (int g = 0; g < G; ++g)
       qv[g] = ld_u32x4(reinterpret_cast<const bf16*>(a.q) + ((size_t)b * a.Hq + kvh * G + g) * kD + 8 * dl);
     const size_t head_off = (size_t)kvh * kD + 8 * dl;
-    auto row_ptr = [&](const bf16* base, int t) {
-      return base + ((size_t)b * a.cap + min(t, last)) * a.Hkv * kD + head_off;
+    const size_t new_off = ((size_t)b * a.Hkv + kvh) * kD + 8 * dl;
+    auto row_ptr = [&](const bf16* base, const void* fresh, int t) {
+      const int tt = min(t, last);
+      return tt == slot ? reinterpret_cast<const bf16*>(fresh) + new_off
+                        : base + ((size_t)b * a.cap + tt) * a.Hkv * kD + head_off;
     };
     float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -396,16 +443,16 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(DecArgs a) {
     u32x4 kc[4], vc[4], kn[4], vn[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      kc[u] = ld_u32x4(row_ptr(ks, t0 + 8 * u + kg));
-      vc[u] = ld_u32x4(row_ptr(vs, t0 + 8 * u + kg));
+      kc[u] = ld_u32x4(row_ptr(ks, a.k_new, t0 + 8 * u + kg));
+      vc[u] = ld_u32x4(row_ptr(vs, a.v_new, t0 + 8 * u + kg));
     }
     for (int it = 0; it < iters; ++it) {
       const int tb = t0 + 32 * it;
       // prefetch the next 32 keys (clamped into the chunk, so always in bounds)
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        kn[u] = ld_u32x4(row_ptr(ks, tb + 32 + 8 * u + kg));
-        vn[u] = ld_u32x4(row_ptr(vs, tb + 32 + 8 * u + kg));
+        kn[u] = ld_u32x4(row_ptr(ks, a.k_new, tb + 32 + 8 * u + kg));
+        vn[u] = ld_u32x4(row_ptr(vs, a.v_new, tb + 32 + 8 * u + kg));
       }
       float s[G][4];
 #pragma unroll
@@ -460,6 +507,13 @@ __global__ __launch_bounds__(256) void decode_bf16_kernel(DecArgs a) {
         vc[u] = vn[u];
       }
     }
+    if (slot >= t0 && slot <= last && kg == 0) {
+      const size_t dst = ((size_t)b * a.cap + slot) * a.Hkv * kD + head_off;
+      st_u32x4(reinterpret_cast<bf16*>(a.k_cache) + dst,
+               ld_u32x4(reinterpret_cast<const bf16*>(a.k_new) + new_off));
+      st_u32x4(reinterpret_cast<bf16*>(a.v_cache) + dst,
+               ld_u32x4(reinterpret_cast<const bf16*>(a.v_new) + new_off));
+    }
     // reduce over the 8 key groups; lanes 0..7 hold the chunk's result
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -487,7 +541,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
   const int bh = blockIdx.x;
   const int b = bh / a.Hq;
   const int lane = threadIdx.x;
-  const int nch = a.offsets[b + 1] - a.offsets[b];
+  const int nch = (eff_len(raw_length(a.lengths, a.positions, b), a.cap) + a.chunk - 1) / a.chunk;
   const float* src = a.partial + (size_t)bh * a.maxc * (2 + kD);
   float M = kNegInf;
   for (int ch = lane; ch < nch; ch += 64) M = fmaxf(M, src[ch * (2 + kD)]);
@@ -542,11 +596,16 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
   a.step_lengths = reinterpret_cast<int32_t*>(ws + align256(sizeof(int) * (size_t)(batch + 1)));
   a.partial = reinterpret_cast<float*>(ws + align256(sizeof(int) * (size_t)(batch + 1)) +
                                        align256(sizeof(int) * (size_t)batch));
-  if (f32)
-    hipLaunchKernelGGL((decode_prep_kernel<4>), dim3(1), dim3(256), 0, stream, a);
-  else
-    hipLaunchKernelGGL((decode_prep_kernel<2>), dim3(1), dim3(256), 0, stream, a);
-  if (positions) a.lengths = a.step_lengths;  // the kernels below attend over positions + 1
+  // The register-streaming bf16 kernel walks the chunks and appends itself;
+  // the LDS-staged kernels (fp32, other head groups) need the prep pass.
+  const bool streaming = !f32 && (a.G == 1 || a.G == 2 || a.G == 4 || a.G == 8);
+  if (!streaming) {
+    if (f32)
+      hipLaunchKernelGGL((decode_prep_kernel<4>), dim3(1), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((decode_prep_kernel<2>), dim3(1), dim3(256), 0, stream, a);
+    if (positions) a.lengths = a.step_lengths;  // the kernels below attend over positions + 1
+  }
   const int upper = batch * a.maxc;
   int gx = (1024 + Hkv - 1) / Hkv;
   if (gx > upper) gx = upper;
