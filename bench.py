@@ -121,9 +121,12 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False):
     # per-kernel durations: HIP events on the launch stream between the
     # launches of a step, over as many steps as were timed, so every kernel
     # runs in the same order and cache state as in the timed loop.  The
-    # backward runs as its three phase entry points here (D by its own
-    # kernel, dq reading it); the timed step fuses D into dq instead.
-    names = ("block_map", "attn_fwd", "attn_bwd_delta", "attn_bwd_dq", "attn_bwd_dkdv")
+    # backward is the product call (dq with D fused in, then dk/dv); dk/dv is
+    # then launched once more on its own through its phase entry point (same
+    # kernel, D from an untimed delta launch), and dq is the difference.
+    names = ("block_map", "attn_fwd", "attn_bwd", "attn_bwd_dkdv")
+    out, lse = ops.attn_fwd(q, k, v, ops.block_map(seg, mask, mode, w.length, w.length), mode, scale)
+    ops.attn_bwd_delta(out, do, lse, ws)
     marks = [_events(len(names) + 1) for _ in range(steps)]
     for ev in marks:
         ev[0].record()
@@ -131,15 +134,14 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False):
         ev[1].record()
         out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
         ev[2].record()
-        ops.attn_bwd_delta(out, do, ws)
+        ops.attn_bwd(q, k, v, out, do, lse, plan, mode, scale)
         ev[3].record()
-        ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, scale, ws, dq)
-        ev[4].record()
         ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv)
-        ev[5].record()
+        ev[4].record()
     torch.cuda.synchronize()
     kern = {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in marks) / steps
             for i, name in enumerate(names)}
+    kern["attn_bwd_dq"] = kern["attn_bwd"] - kern["attn_bwd_dkdv"]
     flops = workloads.attention_flops(w)
     algo = {"attn_fwd": flops["fwd"], "attn_bwd_dq": flops["dq"], "attn_bwd_dkdv": flops["dkdv"]}
     dominant = max(algo, key=lambda name: kern[name])
@@ -265,14 +267,13 @@ def cpu_leg(seconds: float):
 # profiles/traffic.json, which the timed run reports as roofline.traffic.
 # --------------------------------------------------------------------------
 CALIB_BYTES = 512 << 20
-TRAFFIC_KERNELS = {  # bench name -> device kernel (C2: bf16, 2 heads per KV head)
+TRAFFIC_KERNELS = {  # bench name -> device kernels (name prefixes, any template arguments)
     "block_map": ("mf::token_ids_kernel", "mf::tile_runs_kernel", "mf::classify_kernel",
                   "mf::worklist_kernel", "mf::order_kernel"),
-    "attn_fwd": ("mf::attn_fwd_bf16_kernel<2>",),
-    "attn_bwd_delta": ("mf::bwd_delta_kernel<false>",),
-    "attn_bwd_dq": ("mf::bwd_dq_bf16_kernel<2>",),
-    "attn_bwd_dkdv": ("mf::bwd_dkdv_bf16_kernel<2>",),
-    "decode": ("mf::decode_prep_kernel", "mf::decode_bf16_kernel<2>", "mf::decode_combine_kernel<false>"),
+    "attn_fwd": ("mf::attn_fwd_bf16_kernel<",),
+    "attn_bwd_dq": ("mf::bwd_dq_bf16_kernel<",),  # computes D itself in the product call
+    "attn_bwd_dkdv": ("mf::bwd_dkdv_bf16_kernel<",),
+    "decode": ("mf::decode_prep_kernel", "mf::decode_bf16_kernel<", "mf::decode_combine_kernel<"),
 }
 
 
@@ -315,8 +316,8 @@ def traffic_from(fetch_dir: str, write_dir: str) -> dict:
                            "write_kib_per_copy": write[copy] * calls_w,
                            "fetch_scale": f_scale, "write_scale": w_scale}}
     for name, kernels in TRAFFIC_KERNELS.items():
-        fb = sum(fetch.get(k, 0.0) for k in kernels) * 1024 * f_scale
-        wb = sum(write.get(k, 0.0) for k in kernels) * 1024 * w_scale
+        fb = sum(v for k, v in fetch.items() if k.startswith(kernels)) * 1024 * f_scale
+        wb = sum(v for k, v in write.items() if k.startswith(kernels)) * 1024 * w_scale
         workload = "C4" if name == "decode" else "C2"
         out.setdefault(workload, {})[name] = {"fetch_bytes": fb, "write_bytes": wb,
                                               "bytes": fb + wb}

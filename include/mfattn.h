@@ -112,7 +112,8 @@ int mf_attn_fwd(const void* q, const void* k, const void* v, int dtype,
 
 /* Backward of mf_attn_fwd (the JAX-autodiff VJP the reference relies on):
  * dq, dk, dv in the element type of q/k/v; dk/dv summed over each GQA group.
- * `workspace` holds the per-row rowsum(dO * O) (mf_attn_bwd_workspace_bytes).
+ * `workspace` holds two fp32 values per (batch, head, query) row
+ * (mf_attn_bwd_workspace_bytes): -rowsum(dO * O) and lse * log2(e).
  * Deterministic: no atomics, fixed reduction order. */
 size_t mf_attn_bwd_workspace_bytes(int batch, int q_len, int q_heads);
 int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out,
@@ -124,12 +125,14 @@ int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out,
 
 /* The three launches of mf_attn_bwd as separate entry points, for callers
  * that schedule them themselves (e.g. dq and dk/dv on two streams) and for
- * per-kernel timing.  mf_attn_bwd_delta writes rowsum(dO * O) into the
- * workspace; mf_attn_bwd_dq and mf_attn_bwd_dkdv read it, so both must be
- * ordered after it.  Arguments mean what they mean in mf_attn_bwd. */
-int mf_attn_bwd_delta(const void* out, const void* dout, int dtype, int batch,
-                      int q_len, int q_heads, int head_dim, void* workspace,
-                      size_t workspace_bytes, void* stream);
+ * per-kernel timing.  mf_attn_bwd_delta writes the workspace (from O, dO
+ * and the forward's lse); mf_attn_bwd_dq and mf_attn_bwd_dkdv read it, so
+ * both must be ordered after it.  Arguments mean what they mean in
+ * mf_attn_bwd. */
+int mf_attn_bwd_delta(const void* out, const void* dout, const float* lse,
+                      int dtype, int batch, int q_len, int q_heads,
+                      int head_dim, void* workspace, size_t workspace_bytes,
+                      void* stream);
 int mf_attn_bwd_dq(const void* q, const void* k, const void* v,
                    const void* dout, const float* lse, int dtype, int batch,
                    int q_len, int kv_len, int q_heads, int kv_heads,

@@ -19,7 +19,7 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
 hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                            const void* dout, const float* lse, bool f32, int batch, int T, int S,
                            int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
-                           void* dk, void* dv, float* delta, int phases, hipStream_t stream);
+                           void* dk, void* dv, float* workspace, int phases, hipStream_t stream);
 size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk);
 int decode_chunk(bool f32);
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
@@ -173,7 +173,7 @@ int mf_attn_fwd(const void* q, const void* k, const void* v, int dtype, int batc
 
 size_t mf_attn_bwd_workspace_bytes(int batch, int q_len, int q_heads) {
   if (batch < 1 || q_len < 1 || q_heads < 1) return 0;
-  return sizeof(float) * (size_t)batch * q_len * q_heads;
+  return 2 * sizeof(float) * (size_t)batch * q_len * q_heads;  // -D and lse2 per row
 }
 
 namespace {
@@ -188,7 +188,7 @@ int attn_bwd_phases(const void* q, const void* k, const void* v, const void* out
   if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
     return rc;
   const bool need_qkv = phases & 6;
-  if ((need_qkv && (!q || !k || !v || !lse || !plan)) || !dout || !workspace ||
+  if ((need_qkv && (!q || !k || !v || !plan)) || !lse || !dout || !workspace ||
       ((phases & 1) && !out) || ((phases & 2) && !dq) || ((phases & 4) && (!dk || !dv)))
     return fail(MF_ERR_INVALID_ARGUMENT, "%s: a required tensor pointer or the workspace is null",
                 what);
@@ -214,11 +214,11 @@ int mf_attn_bwd(const void* q, const void* k, const void* v, const void* out, co
                          workspace_bytes, 7, stream, "mf_attn_bwd launch");
 }
 
-int mf_attn_bwd_delta(const void* out, const void* dout, int dtype, int batch, int q_len,
-                      int q_heads, int head_dim, void* workspace, size_t workspace_bytes,
-                      void* stream) {
+int mf_attn_bwd_delta(const void* out, const void* dout, const float* lse, int dtype, int batch,
+                      int q_len, int q_heads, int head_dim, void* workspace,
+                      size_t workspace_bytes, void* stream) {
   // the delta phase reads no plan; validate it against a minimal one
-  return attn_bwd_phases(nullptr, nullptr, nullptr, out, dout, nullptr, dtype, batch, q_len, q_len,
+  return attn_bwd_phases(nullptr, nullptr, nullptr, out, dout, lse, dtype, batch, q_len, q_len,
                          q_heads, 1, head_dim, MF_MODE_PACKED_BIDIR, 1.f, nullptr,
                          mf::plan_layout(batch, q_len, q_len).total, nullptr, nullptr, nullptr,
                          workspace, workspace_bytes, 1, stream, "mf_attn_bwd_delta launch");

@@ -1,7 +1,8 @@
 // Backward of the segment-masked flash forward on gfx950.
 //
 // Three deterministic launches (no atomics, fixed reduction order):
-//   1. delta:  D[b,h,t] = sum_d dO * O   (fp32), one thread per (b, t, h).
+//   1. delta:  D[b,h,t] = sum_d dO * O   (fp32), one thread per (b, t, h);
+//              the workspace keeps -D and lse2 = lse * log2(e) per row.
 //   2. dq:     per 128-query tile (like the forward): recompute
 //              S^T = K Q^T and dP^T = V dO^T over the tile's non-empty key
 //              tiles, P^T = exp2(c S^T - lse2), dS^T = P^T (dP^T - D), and
@@ -31,7 +32,8 @@ struct BwdArgs {
   const void* out;
   const void* dout;
   const float* lse;
-  float* delta;
+  float* ndelta;  // workspace: -D per row, [B, Hq, T]
+  float* lse2;    // workspace: lse * log2(e) per row, [B, Hq, T]
   void* dq;
   void* dk;
   void* dv;
@@ -46,7 +48,7 @@ struct BwdArgs {
   int T, S, Hq, Hkv, G, hchunks;
   int nq, nk, tq_pad, tk_pad;
   int causal;
-  int fuse_delta;  // bf16 dq computes D = rowsum(dO * O) itself and writes it
+  int fuse_delta;  // bf16 dq computes D = rowsum(dO * O) itself and writes -D and lse2
   float scale, scale_log2;
 };
 
@@ -88,7 +90,9 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdArgs a, int B) {
       for (int e = 0; e < 4; ++e) acc = fmaf(x[e], y[e], acc);
     }
   }
-  a.delta[((size_t)b * a.Hq + h) * a.T + t] = acc;
+  const size_t li = ((size_t)b * a.Hq + h) * a.T + t;
+  a.ndelta[li] = -acc;
+  a.lse2[li] = a.lse[li] * kLog2e;
 }
 
 // ---------------------------------------------------------------------------
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
     }
     const size_t li = ((size_t)b * a.Hq + head[j]) * a.T + qpos;
     lse2[j] = qactive ? a.lse[li] * kLog2e : kPosInf;
-    dlt[j] = qvalid ? a.delta[li] : 0.f;
+    dlt[j] = qvalid ? -a.ndelta[li] : 0.f;
   }
 
   f32x16 dqacc[HPW][2];
@@ -469,7 +473,7 @@ __device__ __forceinline__ void kv_load(const BwdArgs& a, int b, int h, int qb, 
     const size_t li = ((size_t)b * a.Hq + h) * a.T + qq;
     st.qid = id;
     st.lse2 = act ? a.lse[li] * kLog2e : kPosInf;
-    st.dlt = act ? a.delta[li] : 0.f;
+    st.dlt = act ? -a.ndelta[li] : 0.f;
   }
 }
 
@@ -742,9 +746,12 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
       }
     }
     dlt_raw = halves_sum(part);
-    if (qvalid && half == 0) a.delta[li] = dlt_raw;
+    if (qvalid && half == 0) {
+      a.ndelta[li] = -dlt_raw;
+      a.lse2[li] = lse_raw * kLog2e;
+    }
   } else {
-    dlt_raw = a.delta[li];
+    dlt_raw = -a.ndelta[li];
   }
   drain_memory();
   const float lse2 = qactive ? lse_raw * kLog2e : kPosInf;
@@ -959,8 +966,8 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
       const int s = min(wave >> 1, HS - 1);
       const size_t li = ((size_t)b * a.Hq + kvh * a.G + s + HS * hj) * a.T + qq;
       const void* src = wave == 2 * HS ? (const void*)(a.qid + (size_t)b * a.tq_pad + qb + lane)
-                        : (wave & 1) ? (const void*)(a.delta + li)
-                                     : (const void*)(a.lse + li);
+                        : (wave & 1) ? (const void*)(a.ndelta + li)
+                                     : (const void*)(a.lse2 + li);
       char* dst = wave == 2 * HS ? stage + Q::kIdOff
                   : (wave & 1)   ? stage + Q::kDltOff + s * 256
                                  : stage + Q::kLseOff + s * 256;
@@ -986,15 +993,30 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   const int uk = uniform(mykid);
   const bool kuni = __all(mykid == uk);
 
-  auto block = [&](const char* qt, const char* gt, const float* lse_l, const float* dlt_l,
-                   const int* qid_l, int qb, int qb2, bool mask_ids, bool diag) {
-    f32x16 s = zero16(), dp = zero16();
+  // One 32-query block in three parts: S = Q K^T and dP - D = dO V^T - D
+  // (MFMA, the accumulator starting from the stage's -D), P and dS (VALU),
+  // dV^T += dO^T P and dK^T += Q^T dS (MFMA).
+  auto scores = [&](const char* qt, const char* gt, const float* ndlt_l, int qb2, f32x16& s,
+                    f32x16& dp) {
+    s = zero16();
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const float4 d4 = *reinterpret_cast<const float4*>(&ndlt_l[qb2 * 32 + 8 * g4 + 4 * half]);
+      dp[g4 * 4 + 0] = d4.x;
+      dp[g4 * 4 + 1] = d4.y;
+      dp[g4 * 4 + 2] = d4.z;
+      dp[g4 * 4 + 3] = d4.w;
+    }
     const int qrow = qb2 * 32 + (lane & 31);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       s = mfma32x32x16(tile_chunk(qt, qrow, 2 * ks + half), kf[ks], s);
       dp = mfma32x32x16(tile_chunk(gt, qrow, 2 * ks + half), vf[ks], dp);
     }
+  };
+  auto probs = [&](f32x16& s, f32x16& dp, const float* lse_l, const int* qid_l, int qb, int qb2,
+                   bool mask_ids, bool diag,
+                   bf16x8 (&pf)[2], bf16x8 (&sf)[2]) {
     if (mask_ids) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
@@ -1011,34 +1033,37 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int qq0 = qb2 * 32 + 8 * g4 + 4 * half;
-      const float4 l4 = *reinterpret_cast<const float4*>(&lse_l[qq0]);
-      const float4 d4 = *reinterpret_cast<const float4*>(&dlt_l[qq0]);
+      const float4 l4 = *reinterpret_cast<const float4*>(&lse_l[qb2 * 32 + 8 * g4 + 4 * half]);
       const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-      const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = g4 * 4 + i;
-        // masked scores are -inf and inactive rows have lse = +inf: p = 0
-        const float p = fast_exp2(fmaf(s[r], c, -lv[i] * kLog2e));
+        // lse_l holds lse * log2(e); masked scores are -inf and inactive
+        // rows have lse = +inf: p = 0
+        const float p = fast_exp2(fmaf(s[r], c, -lv[i]));
         s[r] = p;
-        dp[r] = p * (dp[r] - dv4[i]);
+        dp[r] *= p;
       }
     }
-    const bf16x8 pf0 = pack8(s, 0), pf1 = pack8(s, 8);
-    const bf16x8 sf0 = pack8(dp, 0), sf1 = pack8(dp, 8);
+    pf[0] = pack8(s, 0);
+    pf[1] = pack8(s, 8);
+    sf[0] = pack8(dp, 0);
+    sf[1] = pack8(dp, 8);
+  };
+  auto accumulate = [&](const char* qt, const char* gt, int qb2, const bf16x8 (&pf)[2],
+                        const bf16x8 (&sf)[2]) {
     const int r0 = qb2 * 32 + tr_row_of(lane);
     const int cb = tr_col_of(lane);
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
       const bf16x8 g0 = tile_tr_operand(gt, r0, db * 32 + cb);
       const bf16x8 g1 = tile_tr_operand(gt, r0 + 16, db * 32 + cb);
-      dvacc[db] = mfma32x32x16(g0, pf0, dvacc[db]);
-      dvacc[db] = mfma32x32x16(g1, pf1, dvacc[db]);
+      dvacc[db] = mfma32x32x16(g0, pf[0], dvacc[db]);
+      dvacc[db] = mfma32x32x16(g1, pf[1], dvacc[db]);
       const bf16x8 q0 = tile_tr_operand(qt, r0, db * 32 + cb);
       const bf16x8 q1 = tile_tr_operand(qt, r0 + 16, db * 32 + cb);
-      dkacc[db] = mfma32x32x16(q0, sf0, dkacc[db]);
-      dkacc[db] = mfma32x32x16(q1, sf1, dkacc[db]);
+      dkacc[db] = mfma32x32x16(q0, sf[0], dkacc[db]);
+      dkacc[db] = mfma32x32x16(q1, sf[1], dkacc[db]);
     }
   };
 
@@ -1050,25 +1075,39 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     const char* qt = stage + 2 * slot * kTileBytes;
     const char* gt = stage + (2 * slot + 1) * kTileBytes;
     const float* lse_l = reinterpret_cast<const float*>(stage + Q::kLseOff + slot * 256);
-    const float* dlt_l = reinterpret_cast<const float*>(stage + Q::kDltOff + slot * 256);
+    const float* ndlt_l = reinterpret_cast<const float*>(stage + Q::kDltOff + slot * 256);
     const int* qid_l = reinterpret_cast<const int*>(stage + Q::kIdOff);
+    // Both 32-query blocks' score MFMAs are issued before the VALU work of
+    // the first, so the matrix pipe runs block 1's scores under block 0's
+    // exponentials and block 0's accumulation under block 1's.
+    bool run[2] = {true, true}, mask_ids[2] = {false, false}, diag[2] = {false, false};
+    if (partial) {
 #pragma unroll
-    for (int qb2 = 0; qb2 < 2; ++qb2) {
-      bool run = true, mask_ids = false, diag = false;
-      if (partial) {
+      for (int qb2 = 0; qb2 < 2; ++qb2) {
         const int q0 = qb + qb2 * 32;
         const bool above = a.causal && k0 > q0 + 31;
-        diag = a.causal && k0 + 31 > q0;
+        diag[qb2] = a.causal && k0 + 31 > q0;
         if (kuni) {
           const uint64_t m = __ballot(qid_l[qb2 * 32 + (lane & 31)] == uk);
-          run = !above && uk != 0 && m != 0;
-          mask_ids = m != ~0ull;
+          run[qb2] = !above && uk != 0 && m != 0;
+          mask_ids[qb2] = m != ~0ull;
         } else {
-          run = !above;
-          mask_ids = true;
+          run[qb2] = !above;
+          mask_ids[qb2] = true;
         }
       }
-      if (run) block(qt, gt, lse_l, dlt_l, qid_l, qb, qb2, mask_ids, diag);
+    }
+    f32x16 s0, dp0, s1, dp1;
+    bf16x8 pf[2], sf[2];
+    if (run[0]) scores(qt, gt, ndlt_l, 0, s0, dp0);
+    if (run[1]) scores(qt, gt, ndlt_l, 1, s1, dp1);
+    if (run[0]) {
+      probs(s0, dp0, lse_l, qid_l, qb, 0, mask_ids[0], diag[0], pf, sf);
+      accumulate(qt, gt, 0, pf, sf);
+    }
+    if (run[1]) {
+      probs(s1, dp1, lse_l, qid_l, qb, 1, mask_ids[1], diag[1], pf, sf);
+      accumulate(qt, gt, 1, pf, sf);
     }
   };
 
@@ -1145,7 +1184,7 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
 hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                            const void* dout, const float* lse, bool f32, int batch, int T, int S,
                            int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
-                           void* dk, void* dv, float* delta, int phases, hipStream_t stream) {
+                           void* dk, void* dv, float* workspace, int phases, hipStream_t stream) {
   BwdArgs a;
   const PlanLayout lay = plan_layout(batch, T, S);
   const char* p = reinterpret_cast<const char*>(plan);
@@ -1155,7 +1194,8 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   a.out = out;
   a.dout = dout;
   a.lse = lse;
-  a.delta = delta;
+  a.ndelta = workspace;
+  a.lse2 = workspace + (size_t)batch * Hq * T;
   a.dq = dq;
   a.dk = dk;
   a.dv = dv;

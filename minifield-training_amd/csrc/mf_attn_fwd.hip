@@ -418,9 +418,12 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   drain_memory();
 
   f32x16 oacc[2] = {zero16(), zero16()};
-  float m_used = kNegInf, l = 0.f;
+  // Exponentials are taken of x = s*c - shift (base 2).  shift is the running
+  // max in log2 units once a valid key was seen (0 before); it only moves
+  // when a new max exceeds it by more than `lag` (8 once set, -inf before).
+  float shift = 0.f, lag = kNegInf;
+  float l0 = 0.f, l1 = 0.f;  // row-sum partials
   const float c = a.scale_log2;
-  const float tau = 8.f / c;  // lag allowed between m_used and the true max (raw units)
 
   const int count = ld_const(a.qcnt, b * a.nq + qt);
   const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
@@ -472,31 +475,47 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
       for (int r = 0; r < 16; ++r)
         s[r] = kb + kb2 * 32 + acc_row(r, lane) <= qpos ? s[r] : kNegInf;
     }
-    float mx = kNegInf;
+    // shift first: FMA results are canonical, so the max needs no NaN
+    // quieting and folds into v_max3
 #pragma unroll
-    for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[r], s[r + 1]));
+    for (int r = 0; r < 16; ++r) s[r] = fmaf(s[r], c, -shift);
+    float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[r]), s[r + 1]);
     mx = halves_max(mx);
-    const bool grow = mx > m_used + tau;
+    const bool grow = mx > lag;
     if (__any(grow)) {
-      const float mnew = grow ? mx : m_used;
-      // a lane that has seen no valid key yet (m_used = -inf) has l = 0 and
-      // O = 0; give it alpha = 0 rather than exp2(-inf - -inf) = NaN
-      const float alpha = m_used == kNegInf ? 0.f : fast_exp2((m_used - mnew) * c);
-      m_used = mnew;
-      l *= alpha;
+      // a growing lane moves its shift to the new max: d > 0 and finite, so
+      // alpha = 2^-d is finite (a lane with no valid key yet has l = 0, O = 0)
+      const float d = grow ? mx : 0.f;
+      const float alpha = fast_exp2(-d);
+      shift += d;
+      lag = grow ? 8.f : lag;
+      l0 *= alpha;
+      l1 *= alpha;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         oacc[0][r] *= alpha;
         oacc[1][r] *= alpha;
+        s[r] -= d;
       }
     }
-    const float mc = m_used == kNegInf ? 0.f : m_used * c;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      s[r] = fast_exp2(fmaf(s[r], c, -mc));
-      l += s[r];
-    }
+    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(s[r]);
     const bf16x8 p0 = pack8(s, 0), p1 = pack8(s, 8);
+    // row sum of the bf16 probabilities that P V uses: one v_dot2 with
+    // (1, 1) per pair (copied through scalars: __builtin_bit_cast of a
+    // vector element reads element 0 whatever the index, clang 22)
+    {
+      const u32x4 w0 = __builtin_bit_cast(u32x4, p0), w1 = __builtin_bit_cast(u32x4, p1);
+      const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t a0 = w0[j], a1 = w1[j];
+        l0 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a0), ones, l0, false);
+        l1 = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a1), ones, l1, false);
+      }
+    }
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
       const bf16x8 v0 = tile_tr_operand(vt, kb2 * 32 + tr_row, db * 32 + tr_col);
@@ -565,12 +584,13 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 
   const bool qactive = qvalid && myqid != 0;
-  const float lt = halves_sum(l);
+  const float lt = halves_sum(l0 + l1);
   const bool has = qactive && lt > 0.f;
   const float inv = has ? 1.f / lt : 0.f;
   if (qvalid) {
+    // natural-log LSE: shift / log2(e) + ln(l)
     if (half == 0)
-      a.lse[((size_t)b * a.Hq + head) * a.T + qpos] = has ? fmaf(m_used, a.scale, __logf(lt)) : kPosInf;
+      a.lse[((size_t)b * a.Hq + head) * a.T + qpos] = has ? fmaf(shift, kLn2, __logf(lt)) : kPosInf;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll

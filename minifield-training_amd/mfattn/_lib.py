@@ -97,7 +97,7 @@ def _load() -> ctypes.CDLL:
     lib.mf_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                 f32, vp, sz, vp, vp, vp, vp, sz, vp]
     lib.mf_attn_bwd.restype = i32
-    lib.mf_attn_bwd_delta.argtypes = [vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]
+    lib.mf_attn_bwd_delta.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, vp, sz, vp]
     lib.mf_attn_bwd_delta.restype = i32
     lib.mf_attn_bwd_dq.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
                                    f32, vp, sz, vp, vp, sz, vp]

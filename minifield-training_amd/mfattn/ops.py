@@ -156,11 +156,11 @@ def bwd_workspace(q: torch.Tensor) -> torch.Tensor:
                        device=q.device)
 
 
-def attn_bwd_delta(out, dout, ws) -> None:
-    """Phase 1 of the backward: rowsum(dO * O) into ``ws``."""
+def attn_bwd_delta(out, dout, lse, ws) -> None:
+    """Phase 1 of the backward: -rowsum(dO * O) and lse * log2(e) into ``ws``."""
     b, t, hq, d = out.shape
-    _lib.check(_lib.LIB.mf_attn_bwd_delta(_ptr(out), _ptr(dout), dtype_code(out), b, t, hq, d,
-                                          _ptr(ws), ws.numel(), _stream(out.device)))
+    _lib.check(_lib.LIB.mf_attn_bwd_delta(_ptr(out), _ptr(dout), _ptr(lse), dtype_code(out), b, t,
+                                          hq, d, _ptr(ws), ws.numel(), _stream(out.device)))
 
 
 def attn_bwd_dq(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, dq) -> None:

@@ -92,7 +92,7 @@ def test_block_map_and_decode_reject_bad_arguments():
         _lib.ERR_HEADS
     assert L.mf_decode(None, None, None, None, 1, 2, 6, 4, 2, 64, 1.0, None, None, 0, None) == \
         _lib.ERR_INVALID_ARGUMENT
-    assert L.mf_attn_bwd_workspace_bytes(2, 6, 4) == 2 * 6 * 4 * 4
+    assert L.mf_attn_bwd_workspace_bytes(2, 6, 4) == 2 * 2 * 6 * 4 * 4
     assert L.mf_decode_workspace_bytes(64, 8192, 16, 64) > 0
 
 
