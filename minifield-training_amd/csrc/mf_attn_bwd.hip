@@ -951,6 +951,9 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   const float c = a.scale_log2;
   const size_t qrow_stride = (size_t)a.Hq * kD * sizeof(bf16);
 
+  static_assert(W % 8 == 0 || 8 % W == 0, "8-row groups map to tiles statically");
+  const char* const qbase = reinterpret_cast<const char*>(a.q);
+  const char* const gbase = reinterpret_cast<const char*>(a.dout);
   // DMA of iteration `it` (query rows qb .. qb+63 of HS heads) into a stage.
   auto issue = [&](int it, char* stage) {
     it = min(it, niters - 1);
@@ -975,12 +978,13 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < Q::kGroupsPerWave; ++j) {
-      const int g = wave + W * j;              // global 8-row group index
-      const int tile = g >> 3, r0 = 8 * (g & 7);
+      // 8-row group wave + W j: with wave < W and W a divisor or multiple of
+      // 8, its tile (W j) / 8 is a compile-time constant, so the Q / dO
+      // choice is a register select rather than a reload of the argument
+      const int tile = (W * j) >> 3, r0 = 8 * ((wave + W * j) & 7);
       const int s = tile >> 1;                 // head slot of this tile
       const int h = kvh * a.G + s + HS * hj;
-      const char* base = reinterpret_cast<const char*>((tile & 1) ? a.dout : a.q) +
-                         ((size_t)b * a.T * a.Hq + h) * kD * sizeof(bf16);
+      const char* base = ((tile & 1) ? gbase : qbase) + ((size_t)b * a.T * a.Hq + h) * kD * sizeof(bf16);
       dma_rows8(base, qrow_stride, qb, r0, a.T - 1, stage + tile * kTileBytes);
     }
   };
