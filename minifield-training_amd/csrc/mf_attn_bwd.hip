@@ -686,7 +686,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
 
 // ---------------------------------------------------------------------------
 // bf16 dq: the structure of the bf16 forward (one head per wave, 4*HPW
-// waves, K/V tiles DMA'd into a three-stage LDS ring two steps ahead).
+// waves, K/V tiles DMA'd into a two-slot LDS ring of 128-key slots).
 // dQ^T += K^T dS^T takes its K^T operand from the K tile through
 // transposing LDS reads.
 // ---------------------------------------------------------------------------
@@ -694,8 +694,8 @@ template <int HPW>
 __global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2 * HPW)))
 void bwd_dq_bf16_kernel(BwdArgs a) {
   constexpr int W = 4 * HPW;
-  __shared__ __attribute__((aligned(16))) char stage0[kStageBytes], stage1[kStageBytes],
-      stage2[kStageBytes];
+  // two ring slots of 128 keys, each two 64-key stages
+  __shared__ __attribute__((aligned(16))) char slotA[2 * kStageBytes], slotB[2 * kStageBytes];
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int half = lane >> 5;
@@ -843,27 +843,26 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     }
   };
 
-  constexpr int G = KvDma<W>::kPerStep;
-  if (nsteps > 0) {
-    issue(0, stage0);
-    issue(1, stage1);
-  }
-  // Whole groups of three steps; the compute of steps past the end is
-  // skipped rather than leaving the loop mid-group (a mid-group exit gives the
-  // accumulators three exit paths, resolved with register copies).
-  for (int step = 0; step < nsteps; step += 3) {
-    wait_vmcnt<G>();
+  // Ring of two 128-key slots (as in the forward): slot i+1's DMAs are issued
+  // right after the barrier that opens slot i; whole pairs of slots, with the
+  // computes past the end skipped.
+  auto issue_slot = [&](int i, char* slot) {
+    if (2 * i < nsteps) issue(2 * i, slot);
+    if (2 * i + 1 < nsteps) issue(2 * i + 1, slot + kStageBytes);
+  };
+  const int nslots = (nsteps + 1) >> 1;
+  issue_slot(0, slotA);
+  for (int i = 0; i < nslots; i += 2) {
+    wait_vmcnt<0>();
     barrier();
-    issue(step + 2, stage2);
-    compute(step, stage0);
-    wait_vmcnt<G>();
+    issue_slot(i + 1, slotB);
+    compute(2 * i, slotA);
+    if (2 * i + 1 < nsteps) compute(2 * i + 1, slotA + kStageBytes);
+    wait_vmcnt<0>();
     barrier();
-    issue(step + 3, stage0);
-    if (step + 1 < nsteps) compute(step + 1, stage1);
-    wait_vmcnt<G>();
-    barrier();
-    issue(step + 4, stage1);
-    if (step + 2 < nsteps) compute(step + 2, stage2);
+    issue_slot(i + 2, slotA);
+    if (2 * i + 2 < nsteps) compute(2 * i + 2, slotB);
+    if (2 * i + 3 < nsteps) compute(2 * i + 3, slotB + kStageBytes);
   }
   wait_vmcnt<0>();
 
@@ -887,7 +886,8 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
 // process different query heads of the GQA group (slot w/4 takes heads
 // slot, slot+HS, ...), so each query step stages Q and dO of HS heads; their
 // dK/dV are summed through LDS at the end.  Q, dO, lse, D and the query ids
-// are DMA'd into a three-stage LDS ring two steps ahead; dV^T += dO^T P and
+// are DMA'd into a two-slot LDS ring (two 64-query stages per slot, one slot
+// ahead of use); dV^T += dO^T P and
 // dK^T += Q^T dS read their transposed operands from the Q / dO tiles.
 // ---------------------------------------------------------------------------
 template <int HS>
@@ -897,10 +897,6 @@ struct QDma {
   static constexpr int kGroupsPerWave = kTiles * 8 / W;      // 8-row groups
   static constexpr int kWordArrays = 2 * HS + 1;             // lse, D per slot; ids
   static_assert(kWordArrays <= W, "one word array per wave");
-  // Waves below kWordArrays issue one more DMA per step than the others; the
-  // step wait uses the smaller count, which for them also covers the oldest
-  // DMA of the stage issued one step earlier.
-  static constexpr int kPerStep = kGroupsPerWave;
   // stage layout: tiles [slot][Q, dO], then lse[slot][64], D[slot][64], ids[64]
   static constexpr int kLseOff = kTiles * kTileBytes;
   static constexpr int kDltOff = kLseOff + HS * 256;
@@ -913,8 +909,8 @@ __global__ __launch_bounds__(256 * HS) __attribute__((amdgpu_waves_per_eu(2)))
 void bwd_dkdv_bf16_kernel(BwdArgs a) {
   using Q = QDma<HS>;
   constexpr int W = Q::W;
-  __shared__ __attribute__((aligned(16))) char stage0[Q::kStageBytes], stage1[Q::kStageBytes],
-      stage2[Q::kStageBytes];
+  // two ring slots of 128 queries, each two 64-query stages
+  __shared__ __attribute__((aligned(16))) char slotA[2 * Q::kStageBytes], slotB[2 * Q::kStageBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
@@ -1115,38 +1111,38 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     }
   };
 
-  constexpr int G = Q::kPerStep;
-  if (niters > 0) {
-    issue(0, stage0);
-    issue(1, stage1);
-  }
-  // The loop runs whole groups of three steps and skips the compute of the
-  // (at most two) steps past the end: a mid-group exit would give the
-  // accumulators three different exit paths, which the register allocator
+  // Ring of two slots of two iterations each: slot i+1's DMAs are issued
+  // right after the barrier that opens slot i.  The loop runs whole pairs of
+  // slots and skips the computes past the end: a mid-pair exit would give
+  // the accumulators two different exit paths, which the register allocator
   // resolves with 64-register copies.
-  for (int it = 0; it < niters; it += 3) {
-    wait_vmcnt<G>();
+  auto issue_slot = [&](int i, char* slot) {
+    if (2 * i < niters) issue(2 * i, slot);
+    if (2 * i + 1 < niters) issue(2 * i + 1, slot + Q::kStageBytes);
+  };
+  const int nslots = (niters + 1) >> 1;
+  issue_slot(0, slotA);
+  for (int i = 0; i < nslots; i += 2) {
+    wait_vmcnt<0>();
     barrier();
-    issue(it + 2, stage2);
-    compute(it, stage0);
-    wait_vmcnt<G>();
+    issue_slot(i + 1, slotB);
+    compute(2 * i, slotA);
+    if (2 * i + 1 < niters) compute(2 * i + 1, slotA + Q::kStageBytes);
+    wait_vmcnt<0>();
     barrier();
-    issue(it + 3, stage0);
-    if (it + 1 < niters) compute(it + 1, stage1);
-    wait_vmcnt<G>();
-    barrier();
-    issue(it + 4, stage1);
-    if (it + 2 < niters) compute(it + 2, stage2);
+    issue_slot(i + 2, slotA);
+    if (2 * i + 2 < niters) compute(2 * i + 2, slotB);
+    if (2 * i + 3 < niters) compute(2 * i + 3, slotB + Q::kStageBytes);
   }
   wait_vmcnt<0>();
 
   if constexpr (HS == 2) {
-    // slot 1 hands its partial dK (through stage0) and dV (through stage1)
+    // slot 1 hands its partial dK (through ring slot A) and dV (through B)
     // to slot 0; the ring is idle once every wave has passed the barrier
     static_assert(4 * 64 * 32 * sizeof(float) <= Q::kStageBytes, "reduction buffer");
     barrier();
-    float* kred = reinterpret_cast<float*>(stage0) + ((wave & 3) * 64 + lane) * 32;
-    float* vred = reinterpret_cast<float*>(stage1) + ((wave & 3) * 64 + lane) * 32;
+    float* kred = reinterpret_cast<float*>(slotA) + ((wave & 3) * 64 + lane) * 32;
+    float* vred = reinterpret_cast<float*>(slotB) + ((wave & 3) * 64 + lane) * 32;
     if (slot == 1) {
 #pragma unroll
       for (int db = 0; db < 2; ++db)

@@ -377,19 +377,20 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
 // Wave w serves head hc*HPW + w/4 of the KV group and queries
 // [qt*128 + 32 (w%4), +32).  All waves of the workgroup share each 64-key
 // step's K and V tiles (the GQA sharing).  The tiles are DMA'd from HBM into a
-// three-stage LDS ring two steps ahead of use (no staging registers); K feeds
-// the S^T = K Q^T MFMAs directly and V^T is read with transposing LDS reads.
-// Rescaling of the output accumulator is lazy: the running max used for the
-// exponentials only moves when the true max exceeds it by more than 8 in
-// log2 units, so P <= 2^8 and the final division by the row sum is
-// unchanged.  Row sums are fp32 adds (v_dot2 would occupy the matrix pipe).
+// two-slot LDS ring of 128-key slots, one slot ahead of use (no staging
+// registers); K feeds the S^T = K Q^T MFMAs directly and V^T is read with
+// transposing LDS reads.  Rescaling of the output accumulator is lazy: the
+// running max used for the exponentials only moves when the true max exceeds
+// it by more than 8 in log2 units, so P <= 2^8 and the final division by the
+// row sum is unchanged.  Row sums are v_dot2 of the bf16 probabilities with
+// (1, 1), a full-rate VALU op that halves the adds.
 // ---------------------------------------------------------------------------
 template <int HPW>
 __global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2 * HPW)))
 void attn_fwd_bf16_kernel(FwdArgs a) {
   constexpr int W = 4 * HPW;
-  __shared__ __attribute__((aligned(16))) char stage0[kStageBytes], stage1[kStageBytes],
-      stage2[kStageBytes];
+  // two ring slots of 128 keys, each two 64-key stages
+  __shared__ __attribute__((aligned(16))) char slotA[2 * kStageBytes], slotB[2 * kStageBytes];
   const int lane = threadIdx.x & 63;
   // scalar wave index: keeps the DMA destinations scalar expressions of the
   // stage arrays, so the compiler sees which stage each DMA writes
@@ -559,27 +560,29 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     if (run[1]) softmax_pv(s1, vt, kids_lds, kb, 1, mask_ids[1], diag[1]);
   };
 
-  constexpr int G = KvDma<W>::kPerStep;
-  if (nsteps > 0) {
-    issue(0, stage0);
-    issue(1, stage1);
-  }
-  // Whole groups of three steps; the compute of steps past the end is
-  // skipped rather than leaving the loop mid-group (a mid-group exit gives the
-  // accumulators three exit paths, resolved with register copies).
-  for (int step = 0; step < nsteps; step += 3) {
-    wait_vmcnt<G>();
+  // Ring of two 128-key slots: the DMAs of slot i+1 are issued right after
+  // the barrier that opens slot i, so they have the compute of slot i (four
+  // 32-key blocks) to land, and one barrier serves 128 keys.
+  auto issue_slot = [&](int i, char* slot) {
+    if (2 * i < nsteps) issue(2 * i, slot);
+    if (2 * i + 1 < nsteps) issue(2 * i + 1, slot + kStageBytes);
+  };
+  const int nslots = (nsteps + 1) >> 1;
+  issue_slot(0, slotA);
+  // Whole pairs of slots; the computes past the end are skipped rather than
+  // leaving the loop mid-pair (a mid-pair exit gives the accumulators two
+  // exit paths, resolved with register copies).
+  for (int i = 0; i < nslots; i += 2) {
+    wait_vmcnt<0>();
     barrier();
-    issue(step + 2, stage2);
-    compute(step, stage0);
-    wait_vmcnt<G>();
+    issue_slot(i + 1, slotB);
+    compute(2 * i, slotA);
+    if (2 * i + 1 < nsteps) compute(2 * i + 1, slotA + kStageBytes);
+    wait_vmcnt<0>();
     barrier();
-    issue(step + 3, stage0);
-    if (step + 1 < nsteps) compute(step + 1, stage1);
-    wait_vmcnt<G>();
-    barrier();
-    issue(step + 4, stage1);
-    if (step + 2 < nsteps) compute(step + 2, stage2);
+    issue_slot(i + 2, slotA);
+    if (2 * i + 2 < nsteps) compute(2 * i + 2, slotB);
+    if (2 * i + 3 < nsteps) compute(2 * i + 3, slotB + kStageBytes);
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 

@@ -19,7 +19,7 @@
 //
 // The DMAs, the vmcnt waits and the barriers are issued as inline asm with
 // "memory" clobbers, and synchronisation is explicit: a staging loop waits on
-// its own DMAs with vmcnt(N) and then crosses s_barrier.  The compiler is not
+// its own DMAs with vmcnt and then crosses s_barrier.  The compiler is not
 // told about the DMAs on purpose.  Its wait insertion tracks which LDS object
 // a DMA in flight writes only as far as its alias analysis reaches, and when
 // that fails for a later LDS read (which happens for reads in conditionally
@@ -112,10 +112,6 @@ constexpr int kStageBytes = 2 * kTileBytes + 256;  // K tile, V tile, 64 key ids
 template <int W>
 struct KvDma {
   static constexpr int kGroups = 8 / W;            // 8-row groups per tile per wave
-  // Wave 0 also moves the 64 key ids (one DMA, issued first); the step wait
-  // counts only the tile DMAs, which for wave 0 also covers its id DMA of the
-  // stage issued one step earlier.
-  static constexpr int kPerStep = 2 * kGroups;
 };
 
 // DMA of keys kb .. kb+63 (K rows, V rows, canonical ids) into one stage.
