@@ -4,9 +4,11 @@
 
 * step = one pass of the hot path over the C2 batch (LFM2.5-350M encoder
   shape: 8 rows x 4096 tokens, packed bidirectional attention, 16/8 heads,
-  D=64, bf16): block map + flash forward + the three backward launches, with
-  q/k/v/dO resident in HBM.  ``value`` = useful fwd+bwd TFLOP/s
-  (12 * D * Hq * useful pairs per step / time).
+  D=64, bf16): block map + flash forward + the backward (dq with the row
+  sums D fused in, then dk/dv), with q/k/v/dO resident in HBM.  ``value`` =
+  useful fwd+bwd TFLOP/s (12 * D * Hq * useful pairs per step / time) over
+  ``--steps`` steps after ``--warmup`` untimed ones (defaults 100 and 50; the
+  GPU needs ~25 steps to reach its steady clocks).
 * ``roofline`` = the dominant kernel of the step (largest average launch
   duration, timed with HIP events on the launch stream) against the bf16 MFMA
   peak; ``traffic`` comes from the committed rocprofv3 PMC summary when one
@@ -329,8 +331,11 @@ def traffic_from(fetch_dir: str, write_dir: str) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    # The first ~25 steps after launch run ~13% slower while the GPU's clocks
+    # ramp up (measured: 790 us/step for steps 4-23, 690-705 for any later
+    # window of 20-500 steps); 50 warm-up steps (~40 ms) reach steady state.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-step", action="store_true",
