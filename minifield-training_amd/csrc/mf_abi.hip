@@ -86,6 +86,12 @@ int check_attn(int dtype, int batch, int q_len, int kv_len, int q_heads, int kv_
   if (q_heads % kv_heads) return fail(MF_ERR_HEADS, "Query heads must be divisible by KV heads");
   if (head_dim != mf::kD)
     return fail(MF_ERR_HEAD_DIM, "head_dim %d is not supported (kernels serve head_dim 64)", head_dim);
+  // the bf16 kernels address one batch row of q/dO and of k/v with 32-bit
+  // byte offsets (fp32 rows are twice as long; both are checked)
+  if ((size_t)q_len * q_heads * head_dim * 4 >= (size_t(1) << 32) ||
+      (size_t)kv_len * kv_heads * head_dim * 4 >= (size_t(1) << 32))
+    return fail(MF_ERR_SHAPE, "A batch row of q or k/v exceeds 4 GiB (q_len=%d kv_len=%d)", q_len,
+                kv_len);
   const size_t need = mf::plan_layout(batch, q_len, kv_len).total;
   if (plan_bytes < need)
     return fail(MF_ERR_WORKSPACE, "plan holds %zu bytes, %zu needed", plan_bytes, need);

@@ -433,7 +433,7 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   const int tr_row = tr_row_of(lane);
   const int tr_col = tr_col_of(lane);
   const int* kid_row = a.kid + (size_t)b * a.tk_pad;
-  const size_t row_stride = (size_t)a.Hkv * kD * sizeof(bf16);
+  const uint32_t row_stride = (uint32_t)a.Hkv * kD * sizeof(bf16);
   const char* kg = reinterpret_cast<const char*>(a.k) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
   const char* vg = reinterpret_cast<const char*>(a.v) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
 

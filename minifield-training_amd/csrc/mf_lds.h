@@ -15,7 +15,10 @@
 // r & 7 only, every lane's chunk offset is the same for rows 8 apart.
 // A DMA instruction writes lane L's 16 bytes to LDS base + 16 L, so a wave
 // moves 8 rows per instruction; the swizzle is applied on the source side by
-// choosing which global chunk each lane fetches.
+// choosing which global chunk each lane fetches.  Sources are addressed as a
+// wave-uniform 64-bit base in SGPRs plus a 32-bit per-lane byte offset (the
+// instruction's saddr form): one VGPR and 32-bit arithmetic per DMA instead
+// of a 64-bit address.  The launchers keep every offset below 2^32.
 //
 // The DMAs, the vmcnt waits and the barriers are issued as inline asm with
 // "memory" clobbers, and synchronisation is explicit: a staging loop waits on
@@ -52,33 +55,35 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"  // M0 is reserved; see the header comment
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds) : "memory", "m0");
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(src), "s"(lds) : "memory", "m0");
+__device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
 // Tile rows r0 .. r0+7 = global rows first + r0 .. first + r0 + 7 (global
 // row 0 at g_base, rows row_stride bytes apart; rows past `last` re-read row
-// `last`, so every access stays inside the tensor) into the LDS tile.  The
-// tile address and r0 must be wave-uniform.
-__device__ __forceinline__ void dma_rows8(const char* g_base, size_t row_stride, int first, int r0,
-                                          int last, char* tile) {
+// `last`, so every access stays inside the tensor) into the LDS tile.  g_base,
+// the tile address and r0 must be wave-uniform; last * row_stride + 128 must
+// stay below 2^32.
+__device__ __forceinline__ void dma_rows8(const char* g_base, uint32_t row_stride, int first,
+                                          int r0, int last, char* tile) {
   const int lane = __lane_id();
   const int r = r0 + (lane >> 3);
   const int c = (lane & 7) ^ swz(r);
-  const char* src = g_base + (size_t)min(first + r, last) * row_stride + c * 16;
-  dma16(src, uniform((int)lds_offset(tile + r0 * kRowBytes)));
+  const uint32_t voff = (uint32_t)min(first + r, last) * row_stride + (uint32_t)(c * 16);
+  dma16(g_base, voff, uniform((int)lds_offset(tile + r0 * kRowBytes)));
 }
 
-// One 4-byte word per lane, all 64 lanes: lane L's word (read from its own
-// address `src`) lands at dst + 4 L (dst wave-uniform).
-__device__ __forceinline__ void dma_word64(const void* src, void* dst) {
-  dma4(src, uniform((int)lds_offset(dst)));
+// One 4-byte word per lane, all 64 lanes: lane L's word at byte offset
+// voff (per lane) from the wave-uniform base lands at dst + 4 L (dst
+// wave-uniform).
+__device__ __forceinline__ void dma_word64(const void* sbase, uint32_t voff, void* dst) {
+  dma4(sbase, voff, uniform((int)lds_offset(dst)));
 }
 
 // 16-byte operand: chunk c of row r.
@@ -117,9 +122,9 @@ struct KvDma {
 // DMA of keys kb .. kb+63 (K rows, V rows, canonical ids) into one stage.
 // kid_row must hold at least kb + 64 entries (the plan pads ids to whole tiles).
 template <int W>
-__device__ __forceinline__ void kv_dma(const char* kg, const char* vg, size_t row_stride, int S,
+__device__ __forceinline__ void kv_dma(const char* kg, const char* vg, uint32_t row_stride, int S,
                                        const int* kid_row, int kb, int wave, char* stage) {
-  if (wave == 0) dma_word64(kid_row + kb + __lane_id(), stage + 2 * kTileBytes);
+  if (wave == 0) dma_word64(kid_row + kb, 4u * __lane_id(), stage + 2 * kTileBytes);
 #pragma unroll
   for (int j = 0; j < KvDma<W>::kGroups; ++j) {
     const int r0 = 8 * (wave + W * j);
