@@ -30,73 +30,92 @@ struct MapArgs {
   int batch, q_len, kv_len;
   PlanLayout lay;
   char* plan;
+  int ids_ready;  // qid/kid already hold the canonical ids (key-mask mode, placements)
 };
 
 __device__ __forceinline__ int* plan_i32(char* plan, size_t off) {
   return reinterpret_cast<int*>(plan + off);
 }
 
-// One block per (position chunk, row).
+// Key-mask mode ids, one block per (position chunk, row): every query of a
+// row with at least one active key gets id 1 (present = any(mask[b, :]),
+// bidirectional.py:23), key j gets id 1 iff mask != 0.  The packed modes'
+// ids are derived inside the run pass instead.
 __global__ __launch_bounds__(256) void token_ids_kernel(MapArgs a) {
   const int b = blockIdx.y;
   const int p = blockIdx.x * blockDim.x + threadIdx.x;
   int* qid = plan_i32(a.plan, a.lay.qid) + (size_t)b * a.lay.tq_pad;
   int* kid = plan_i32(a.plan, a.lay.kid) + (size_t)b * a.lay.tk_pad;
-  if (a.mode == 2) {
-    // present = any(mask[b, :]) over the key axis (bidirectional.py:23).
-    int any = 0;
-    for (int j = threadIdx.x; j < a.kv_len; j += blockDim.x)
-      any |= mask_at(a.mask, a.mask_u8, (long)b * a.kv_len + j) != 0;
-    any = __syncthreads_or(any);
-    if (p < a.lay.tq_pad) qid[p] = (p < a.q_len && any) ? 1 : 0;
-    if (p < a.lay.tk_pad)
-      kid[p] = (p < a.kv_len && mask_at(a.mask, a.mask_u8, (long)b * a.kv_len + p) != 0) ? 1 : 0;
-    return;
-  }
-  // packed modes: q_len == kv_len, one id per token
-  const int pad = a.lay.tq_pad > a.lay.tk_pad ? a.lay.tq_pad : a.lay.tk_pad;
-  if (p >= pad) return;
-  int id = 0;
-  if (p < a.q_len) {
-    const long idx = (long)b * a.q_len + p;
-    const int m = mask_at(a.mask, a.mask_u8, idx);
-    const int s = a.seg[idx];
-    const bool active = (a.mode == 0 ? m > 0 : m != 0) && s != 0;
-    id = active ? s : 0;
-  }
-  if (p < a.lay.tq_pad) qid[p] = id;
-  if (p < a.lay.tk_pad) kid[p] = id;
+  int any = 0;
+  for (int j = threadIdx.x; j < a.kv_len; j += blockDim.x)
+    any |= mask_at(a.mask, a.mask_u8, (long)b * a.kv_len + j) != 0;
+  any = __syncthreads_or(any);
+  if (p < a.lay.tq_pad) qid[p] = (p < a.q_len && any) ? 1 : 0;
+  if (p < a.lay.tk_pad)
+    kid[p] = (p < a.kv_len && mask_at(a.mask, a.mask_u8, (long)b * a.kv_len + p) != 0) ? 1 : 0;
+}
+
+// Canonical id of token p of row b in the packed modes (q_len == kv_len).
+__device__ __forceinline__ int packed_id(const MapArgs& a, int b, int p) {
+  if (p >= a.q_len) return 0;
+  const long idx = (long)b * a.q_len + p;
+  const int m = mask_at(a.mask, a.mask_u8, idx);
+  const int s = a.seg[idx];
+  const bool active = (a.mode == 0 ? m > 0 : m != 0) && s != 0;
+  return active ? s : 0;
 }
 
 // One wave per (tile, row): tiles [0, nq) are query tiles, [nq, nq+nk) key
-// tiles.  Writes the ordered maximal runs of equal nonzero ids.
+// tiles.  Writes the ordered maximal runs of equal nonzero ids.  In the
+// packed modes it also derives the tile's canonical ids from the segment ids
+// and mask and stores them (query tiles into qid, key tiles into kid), so no
+// separate id pass runs.
 __global__ __launch_bounds__(64) void tile_runs_kernel(MapArgs a) {
   const int b = blockIdx.y;
   const int t = blockIdx.x;
   const int lane = threadIdx.x;
   const bool is_q = t < a.lay.nq;
   const int tile = is_q ? t : t - a.lay.nq;
-  const int* ids = is_q ? plan_i32(a.plan, a.lay.qid) + (size_t)b * a.lay.tq_pad
-                        : plan_i32(a.plan, a.lay.kid) + (size_t)b * a.lay.tk_pad;
+  int* ids = is_q ? plan_i32(a.plan, a.lay.qid) + (size_t)b * a.lay.tq_pad
+                  : plan_i32(a.plan, a.lay.kid) + (size_t)b * a.lay.tk_pad;
   const size_t rec_bytes = sizeof(int) + sizeof(Run) * kMaxRuns;
   char* rec = a.plan + a.lay.runs +
               rec_bytes * ((size_t)b * (a.lay.nq + a.lay.nk) + (size_t)t);
   Run* runs = reinterpret_cast<Run*>(rec + sizeof(int));
   const int p0 = tile * kTile;
+  int x[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    const int p = p0 + half * 64 + lane;
+    if (a.ids_ready) {
+      x[half] = ids[p];
+    } else {
+      x[half] = packed_id(a, b, p);
+      ids[p] = x[half];
+    }
+  }
   int n_start = 0, n_stop = 0;
+#pragma unroll
   for (int half = 0; half < 2; ++half) {
     const int i = half * 64 + lane;
-    const int x = ids[p0 + i];
-    const int prev = i > 0 ? ids[p0 + i - 1] : 0;
-    const int next = i < kTile - 1 ? ids[p0 + i + 1] : 0;
-    const bool st = x != 0 && (i == 0 || prev != x);
-    const bool sp = x != 0 && (i == kTile - 1 || next != x);
+    const int xv = x[half];
+    // neighbours within the tile (the value each source lane offers is
+    // chosen for the reader it serves): token i - 1 is lane - 1 of the same
+    // half, or for half 1 lane 0 the last token of half 0 (lane 63, x[0]);
+    // token i + 1 is lane + 1, or for half 0 lane 63 the first token of half
+    // 1 (lane 0, x[1])
+    const int up = __shfl(half == 0 ? x[0] : (lane == 63 ? x[0] : x[1]), lane == 0 ? 63 : lane - 1);
+    const int dn = __shfl(half == 0 ? (lane == 0 ? x[1] : x[0]) : x[1], lane == 63 ? 0 : lane + 1);
+    const int prev = i > 0 ? up : 0;
+    const int next = i < kTile - 1 ? dn : 0;
+    const bool st = xv != 0 && (i == 0 || prev != xv);
+    const bool sp = xv != 0 && (i == kTile - 1 || next != xv);
     const uint64_t bs = __ballot(st);
     const uint64_t bp = __ballot(sp);
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     if (st) {
       const int k = n_start + __popcll(bs & below);
-      runs[k].id = x;
+      runs[k].id = xv;
       runs[k].start = p0 + i;
     }
     if (sp) {
@@ -284,6 +303,7 @@ hipError_t launch_block_map_placements(const int32_t* placements, int count, int
   a.kv_len = length;
   a.lay = plan_layout(batch, length, length);
   a.plan = reinterpret_cast<char*>(plan);
+  a.ids_ready = 1;
   hipLaunchKernelGGL(placement_clear_kernel, dim3((a.lay.tq_pad + 255) / 256, batch), dim3(256), 0,
                      stream, a, seg_out, pos_out);
   if (count > 0)
@@ -306,8 +326,13 @@ hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, i
   a.kv_len = kv_len;
   a.lay = plan_layout(batch, q_len, kv_len);
   a.plan = reinterpret_cast<char*>(plan);
-  const int pad = a.lay.tq_pad > a.lay.tk_pad ? a.lay.tq_pad : a.lay.tk_pad;
-  hipLaunchKernelGGL(token_ids_kernel, dim3((pad + 255) / 256, batch), dim3(256), 0, stream, a);
+  // packed modes: the run pass derives the ids itself; the key-mask mode
+  // needs a row-wide "any key active" first
+  a.ids_ready = mode == 2;
+  if (a.ids_ready) {
+    const int pad = a.lay.tq_pad > a.lay.tk_pad ? a.lay.tq_pad : a.lay.tk_pad;
+    hipLaunchKernelGGL(token_ids_kernel, dim3((pad + 255) / 256, batch), dim3(256), 0, stream, a);
+  }
   launch_map_tail(a, stream);
   return hipGetLastError();
 }
