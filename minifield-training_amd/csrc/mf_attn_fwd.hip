@@ -1,11 +1,12 @@
 // Flash-style forward for segment-masked GQA attention on gfx950.
 //
-// Work unit: one workgroup = 4 waves = one 128-query tile of one row, for
-// HPW (1 or 2) query heads that share a KV head.  Each wave owns 32 queries
-// for all HPW heads, so every K / V^T fragment it reads from LDS feeds HPW
-// MFMAs (the GQA sharing of K/V tiles).  The workgroup walks the compacted
-// list of non-empty 128-key tiles of its query tile (from the block map) in
-// 64-key steps, double-buffering K and V^T in LDS.
+// Two kernels: the bf16 one (further below; the benchmarked path) and an
+// fp32 template.  fp32 work unit: one workgroup = 4 waves = one 128-query
+// tile of one row, for HPW (1 or 2) query heads that share a KV head.  Each
+// wave owns 32 queries for all HPW heads, so every K / V^T fragment it reads
+// from LDS feeds HPW MFMAs (the GQA sharing of K/V tiles).  The workgroup
+// walks the compacted list of non-empty 128-key tiles of its query tile (from
+// the block map) in 64-key steps, double-buffering K and V^T in LDS.
 //
 // Scores are formed transposed, S^T = K Q^T, so an accumulator column is one
 // query: the row max and row sum are in-lane reductions plus one
