@@ -64,6 +64,8 @@ def _msg():
         (dict(mode=5), _lib.ERR_MODE, "mode"),
         (dict(b=0), _lib.ERR_INVALID_ARGUMENT, "positive"),
         (dict(plan_bytes=16), _lib.ERR_WORKSPACE, "plan holds 16 bytes"),
+        # the kernels' 32-bit DMA offsets cover one batch row of q and of k/v
+        (dict(t=1 << 20, s=1 << 20, hq=16, hkv=8), _lib.ERR_SHAPE, "exceeds 4 GiB"),
         (dict(), _lib.ERR_INVALID_ARGUMENT, "non-null"),
     ],
 )
