@@ -286,3 +286,38 @@ def test_head_dim_padding_path(device):
         attention.dense_packed_causal_attention(
             torch.zeros(1, 8, 2, 128, device=device), torch.zeros(1, 8, 2, 128, device=device),
             torch.zeros(1, 8, 2, 128, device=device), ts[:1, :8] * 0 + 1, ts[:1, :8] * 0 + 1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_phase_entry_points_match_the_fused_backward(dtype, device):
+    """mf_attn_bwd_delta / _dq / _dkdv in sequence give the fused backward's gradients, and the
+    delta phase leaves -rowsum(dO * O) and lse * log2(e) in the workspace."""
+    w = packing.make_workload("C1") if dtype == torch.float32 else packing.make_workload("C2")
+    say(f"phase entry points {w.name} {dtype}")
+    rng = np.random.default_rng(13)
+    q, k, v, do = operands(rng, w.batch, w.length, w.q_heads, w.kv_heads, 64, dtype, 0.5)
+    mode = _lib.MODE_PACKED_CAUSAL if w.causal else _lib.MODE_PACKED_BIDIR
+    tm = torch.tensor(w.attention_mask, device=device)
+    ts = torch.tensor(w.segment_ids, device=device)
+    plan = ops.block_map(ts, tm, mode, w.length, w.length)
+    out, lse = ops.attn_fwd(q, k, v, plan, mode, 0.125)
+    fused = ops.attn_bwd(q, k, v, out, do, lse, plan, mode, 0.125)
+    ws = ops.bwd_workspace(q)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ops.attn_bwd_delta(out, do, lse, ws)
+    ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, 0.125, ws, dq)
+    ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, 0.125, ws, dk, dv)
+    rows = w.batch * w.q_heads * w.length
+    words = ws.view(torch.float32)
+    ndelta = words[:rows].view(w.batch, w.q_heads, w.length)
+    lse2 = words[rows:2 * rows].view(w.batch, w.q_heads, w.length)
+    d_ref = (do.float() * out.float()).sum(-1).permute(0, 2, 1)
+    torch.testing.assert_close(-ndelta, d_ref, rtol=1e-5, atol=1e-5)
+    assert torch.equal(lse2, lse * float(np.float32(np.log2(np.e))))
+    # the fused dq computes D with a different summation order: bf16 gradients agree to
+    # the bf16 bar, fp32 ones to the fp32 bar
+    for a, r in zip((dq, dk, dv), fused):
+        if dtype == torch.float32:
+            torch.testing.assert_close(a, r, rtol=1e-5, atol=1e-5)
+        else:
+            assert bf16_scaled_error(a, r) < BF16_TOL
