@@ -31,7 +31,7 @@ def test_reference_fixtures_on_the_device(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("k", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("mode", ["centered", "causal"])
 def test_random_layouts(dtype, k, mode, device):
     rng = np.random.default_rng(30 + k)
