@@ -15,6 +15,11 @@
   exists for that kernel and workload, else null.
 * ``decode`` = the C4 ragged KV-cached decode (64 x 1 token, cache lengths
   U[128, 8192]): algorithmic HBM GB/s and its roofline fraction.
+* ``rows`` = the kernels either side of the attention path (QK-norm+RoPE
+  prologue, segment positions, segmented conv, decode with the KV append,
+  block map from placements) at the same shapes, each timed over
+  back-to-back C-ABI calls: microseconds, and algorithmic GB/s against the
+  HBM peak for the streaming ones.
 * ``cpu_baseline`` = the reference's dense bidirectional path restated in
   torch on the host cores (XLA-SDPA cast points: fp32 logits, bf16
   probabilities; fwd + autograd bwd), timed per (row, KV-group) chunk of the
@@ -205,6 +210,122 @@ def decode_leg(steps: int, warmup: int, profile: bool = False):
                          "frac": gbps / HBM_PEAK_GBPS, "traffic": _traffic("decode", "C4")}}
 
 
+def _time_batch(fn, iters: int) -> float:
+    """Average ms of ``iters`` back-to-back calls between two events on the launch stream.
+
+    The calls go straight to the C ABI with pointers computed beforehand, so
+    the host enqueues faster than the GPU drains and the average is the
+    kernels' own time (the first call's launch latency is spread over all).
+    """
+    import torch
+
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    start, end = _events(2)
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def rows_leg(steps: int, profile: bool = False):
+    """The kernels on either side of the attention path at the bench shapes.
+
+    qk_norm_rope, segment_positions and segmented_conv run on the C2 layout
+    (8 x 4096 packed tokens, 16/8 heads of 64, an encoder conv over 1024
+    channels), decode_append on C4 (each row appends at its cache length, then
+    decodes), block_map_placements on the placements of C2's segments.
+    ``bytes`` counts each input read and each output written once.
+    """
+    import numpy as np
+    import torch
+
+    from mfattn import _lib, ops, workloads
+
+    L = _lib.LIB
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    p = lambda t: t.data_ptr()  # noqa: E731
+    w = workloads.packed("C2")
+    b, t = w.batch, w.length
+    g = torch.Generator(device=dev).manual_seed(w.seed)
+    bf = torch.bfloat16
+    seg = torch.tensor(w.segment_ids, device=dev, dtype=torch.int32)
+    pos = torch.empty_like(seg)
+    rows = {}
+
+    def run(name, fn, nbytes, bound="hbm", workload="C2"):
+        if profile:
+            fn()
+            torch.cuda.synchronize()
+            return
+        ms = _time_batch(fn, max(steps, 20))
+        entry = {"workload": workload, "us": ms * 1e3, "bound": bound}
+        if nbytes:
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            entry.update(bytes=nbytes, GBps=gbps, frac=gbps / HBM_PEAK_GBPS,
+                         traffic=_traffic(name, workload))
+        rows[name] = entry
+
+    run("segment_positions", lambda: _lib.check(L.mf_segment_positions(p(seg), b, t, p(pos), stream)),
+        0, "latency")
+    q = torch.randn(b, t, w.q_heads, w.head_dim, generator=g, device=dev).to(bf)
+    k = torch.randn(b, t, w.kv_heads, w.head_dim, generator=g, device=dev).to(bf)
+    qg = (1 + 0.1 * torch.randn(w.head_dim, generator=g, device=dev)).to(bf)
+    kg = (1 + 0.1 * torch.randn(w.head_dim, generator=g, device=dev)).to(bf)
+    qo, ko = torch.empty_like(q), torch.empty_like(k)
+    run("qk_norm_rope", lambda: _lib.check(L.mf_qk_norm_rope(
+        p(q), p(k), p(qg), p(kg), p(pos), _lib.DTYPE_BF16, b, t, w.q_heads, w.kv_heads, w.head_dim,
+        1e-5, 1e6, p(qo), p(ko), stream)), 2 * (q.nbytes + k.nbytes) + pos.nbytes)
+    del q, k, qo, ko
+    ch, taps = 1024, 3
+    x = [torch.randn(b, t, ch, generator=g, device=dev).to(bf) for _ in range(3)]
+    wt = (0.5 * torch.randn(ch, taps, generator=g, device=dev)).to(bf)
+    y = torch.empty_like(x[0])
+    run("segmented_conv", lambda: _lib.check(L.mf_segmented_conv(
+        p(x[0]), p(x[1]), p(x[2]), p(wt), p(seg), _lib.CONV_CENTERED, _lib.DTYPE_BF16, b, t, ch, taps,
+        p(y), stream)), 4 * y.nbytes + seg.nbytes + wt.nbytes)
+    del x, y
+    runs = []
+    for r in range(b):
+        ids = w.segment_ids[r]
+        edges = np.flatnonzero(np.diff(np.concatenate(([0], ids, [0]))) != 0)
+        runs += [(r, int(s), int(e - s)) for s, e in zip(edges[:-1], edges[1:]) if ids[s] != 0]
+    pl = torch.tensor(runs, device=dev, dtype=torch.int32)
+    plan_bytes = L.mf_plan_bytes(b, t, t)
+    plan = torch.empty(plan_bytes, dtype=torch.uint8, device=dev)
+    seg2, pos2 = torch.empty_like(seg), torch.empty_like(seg)
+    run("block_map_placements", lambda: _lib.check(L.mf_block_map_placements(
+        p(pl), pl.shape[0], _lib.MODE_PACKED_BIDIR, b, t, p(plan), plan_bytes, p(seg2), p(pos2),
+        stream)), 0, "latency")
+    del plan
+    d = workloads.decode("C4")
+    gq, gc = (d.batch, 1, d.q_heads, d.head_dim), (d.batch, d.capacity, d.kv_heads, d.head_dim)
+    dq = torch.randn(gq, generator=g, device=dev).to(bf)
+    kn = torch.randn(d.batch, 1, d.kv_heads, d.head_dim, generator=g, device=dev).to(bf)
+    vn = torch.randn_like(kn)
+    kc = torch.randn(gc, generator=g, device=dev).to(bf)
+    vc = torch.randn(gc, generator=g, device=dev).to(bf)
+    at = np.minimum(np.asarray(d.valid_length, np.int64), d.capacity - 1)
+    positions = torch.tensor(at, device=dev, dtype=torch.int32)
+    out = torch.empty_like(dq)
+    ws_bytes = L.mf_decode_workspace_bytes(d.batch, d.capacity, d.q_heads, d.head_dim)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    kv_row = d.kv_heads * d.head_dim * 2
+    nbytes = (int((at + 1).sum()) * 2 * kv_row + 2 * dq.nbytes + positions.nbytes
+              + 2 * (kn.nbytes + vn.nbytes))
+    run("decode_append", lambda: _lib.check(L.mf_decode_append(
+        p(dq), p(kn), p(vn), p(positions), _lib.DTYPE_BF16, d.batch, d.capacity, d.q_heads,
+        d.kv_heads, d.head_dim, d.head_dim ** -0.5, p(kc), p(vc), p(out), p(ws), ws_bytes, stream)),
+        nbytes, workload="C4")
+    del dq, kn, vn, kc, vc, out, ws
+    torch.cuda.empty_cache()
+    return None if profile else rows
+
+
 def cpu_leg(seconds: float):
     """Dense reference path on the host, per (row, KV-group) chunk of C2."""
     import numpy as np
@@ -263,8 +384,8 @@ def cpu_leg(seconds: float):
 #   python3 bench.py --traffic gpurun_out/pmc_fetch gpurun_out/pmc_write
 #
 # --profile-step runs one device-to-device copy of CALIB_BYTES (the
-# calibration: it reads and writes exactly that many bytes), one C2 step and
-# one C4 decode.  --traffic scales each kernel's FETCH_SIZE / WRITE_SIZE
+# calibration: it reads and writes exactly that many bytes), one C2 step,
+# one C4 decode and one call of each ``rows`` kernel.  --traffic scales each kernel's FETCH_SIZE / WRITE_SIZE
 # (KiB per dispatch) by what the counters read for the copy and writes
 # profiles/traffic.json, which the timed run reports as roofline.traffic.
 # --------------------------------------------------------------------------
@@ -276,6 +397,8 @@ TRAFFIC_KERNELS = {  # bench name -> device kernels (name prefixes, any template
     "attn_bwd_dq": ("mf::bwd_dq_bf16_kernel<",),  # computes D itself in the product call
     "attn_bwd_dkdv": ("mf::bwd_dkdv_bf16_kernel<",),
     "decode": ("mf::decode_prep_kernel", "mf::decode_bf16_kernel<", "mf::decode_combine_kernel<"),
+    "qk_norm_rope": ("mf::qk_norm_rope_kernel<",),
+    "segmented_conv": ("mf::segmented_conv_kernel<",),
 }
 
 
@@ -289,6 +412,7 @@ def profile_step() -> None:
     torch.cuda.synchronize()
     del src, dst
     gpu_leg(1, 0, profile=True)
+    rows_leg(0, profile=True)
 
 
 def _counter_means(path: pathlib.Path) -> dict:
@@ -298,6 +422,9 @@ def _counter_means(path: pathlib.Path) -> dict:
     sums, counts = {}, {}
     for row in csv.DictReader(open(path)):
         name = re.sub(r"\(.*", "", row["Kernel_Name"]).replace("void ", "").strip()
+        mangled = re.match(r"_ZN2mf(\d+)", name)  # left mangled when a template argument is __bf16
+        if mangled:
+            name = "mf::" + name[mangled.end():mangled.end() + int(mangled.group(1))] + "<"
         key = (name, int(row.get("Dispatch_Id", 0) or 0))
         sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
     per_kernel = {}
@@ -339,7 +466,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-step", action="store_true",
-                    help="run the calibration copy, one C2 step and one C4 decode (for rocprofv3 --pmc)")
+                    help="run the calibration copy, one C2 step, one C4 decode and the rows once "
+                         "(for rocprofv3 --pmc)")
     ap.add_argument("--traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two PMC runs of --profile-step into profiles/traffic.json")
     args = ap.parse_args()
@@ -372,6 +500,7 @@ def main() -> int:
         "cpu_baseline": None if args.no_cpu_baseline else cpu_leg(args.cpu_seconds),
         "decode": gpu["decode"],
         "kernels_ms": gpu["kernels_ms"],
+        "rows": rows_leg(args.steps),
         "fa2_convention_tflops": gpu["fa2_convention_tflops"],
         "step_roofline_frac": gpu["step_roofline_frac"],
         "wall_ms_per_step": gpu["wall_ms_per_step"],
