@@ -391,8 +391,8 @@ def cpu_leg(seconds: float):
 # --------------------------------------------------------------------------
 CALIB_BYTES = 512 << 20
 TRAFFIC_KERNELS = {  # bench name -> device kernels (name prefixes, any template arguments)
-    "block_map": ("mf::token_ids_kernel", "mf::tile_runs_kernel", "mf::classify_kernel",
-                  "mf::worklist_kernel", "mf::order_kernel"),
+    "block_map": ("mf::token_ids_kernel", "mf::tile_runs_kernel", "mf::tile_lists_kernel",
+                  "mf::order_kernel"),
     "attn_fwd": ("mf::attn_fwd_bf16_kernel<",),
     "attn_bwd_dq": ("mf::bwd_dq_bf16_kernel<",),  # computes D itself in the product call
     "attn_bwd_dkdv": ("mf::bwd_dkdv_bf16_kernel<",),

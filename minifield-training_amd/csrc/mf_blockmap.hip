@@ -128,55 +128,57 @@ __global__ __launch_bounds__(64) void tile_runs_kernel(MapArgs a) {
   if (lane == 0) *reinterpret_cast<int*>(rec) = n_start;
 }
 
-// One thread per (q tile, k tile) pair of a row.
-__global__ __launch_bounds__(256) void classify_kernel(MapArgs a) {
-  const int b = blockIdx.y;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+// Class of tile pair (qi, kj) of row b: 0 EMPTY, 1 PARTIAL, 2 FULL, from the
+// two tiles' run lists (a pair is non-empty iff some query run and key run
+// share an id, with the key run starting at or before the query run's last
+// token when causal; FULL iff both tiles are one run of the same id and the
+// pair lies below the causal diagonal).
+__device__ __forceinline__ int pair_class(const MapArgs& a, int b, int qi, int kj) {
   const int nq = a.lay.nq, nk = a.lay.nk;
-  if (idx >= nq * nk) return;
-  const int qi = idx / nk, kj = idx % nk;
   const bool causal = a.mode == 0;
-  uint8_t cls = 0;
-  if (!(causal && kj > qi)) {
-    const size_t rec_bytes = sizeof(int) + sizeof(Run) * kMaxRuns;
-    const char* base = a.plan + a.lay.runs + rec_bytes * ((size_t)b * (nq + nk));
-    const char* rq_rec = base + rec_bytes * qi;
-    const char* rk_rec = base + rec_bytes * (nq + kj);
-    const int nrq = *reinterpret_cast<const int*>(rq_rec);
-    const int nrk = *reinterpret_cast<const int*>(rk_rec);
-    const Run* rq = reinterpret_cast<const Run*>(rq_rec + sizeof(int));
-    const Run* rk = reinterpret_cast<const Run*>(rk_rec + sizeof(int));
-    bool any = false;
-    for (int x = 0; x < nrq && !any; ++x) {
-      const Run u = rq[x];
-      for (int y = 0; y < nrk; ++y) {
-        const Run w = rk[y];
-        if (u.id == w.id && (!causal || w.start <= u.stop - 1)) {
-          any = true;
-          break;
-        }
+  if (causal && kj > qi) return 0;
+  const size_t rec_bytes = sizeof(int) + sizeof(Run) * kMaxRuns;
+  const char* base = a.plan + a.lay.runs + rec_bytes * ((size_t)b * (nq + nk));
+  const char* rq_rec = base + rec_bytes * qi;
+  const char* rk_rec = base + rec_bytes * (nq + kj);
+  const int nrq = *reinterpret_cast<const int*>(rq_rec);
+  const int nrk = *reinterpret_cast<const int*>(rk_rec);
+  const Run* rq = reinterpret_cast<const Run*>(rq_rec + sizeof(int));
+  const Run* rk = reinterpret_cast<const Run*>(rk_rec + sizeof(int));
+  bool any = false;
+  for (int x = 0; x < nrq && !any; ++x) {
+    const Run u = rq[x];
+    for (int y = 0; y < nrk; ++y) {
+      const Run w = rk[y];
+      if (u.id == w.id && (!causal || w.start <= u.stop - 1)) {
+        any = true;
+        break;
       }
     }
-    if (any) {
-      cls = 1;
-      if (nrq == 1 && nrk == 1 && rq[0].id == rk[0].id &&
-          rq[0].start == qi * kTile && rq[0].stop == (qi + 1) * kTile &&
-          rk[0].start == kj * kTile && rk[0].stop == (kj + 1) * kTile &&
-          (!causal || kj < qi))
-        cls = 2;
-    }
   }
-  reinterpret_cast<uint8_t*>(a.plan + a.lay.tmap)[((size_t)b * nq + qi) * nk + kj] = cls;
+  if (!any) return 0;
+  if (nrq == 1 && nrk == 1 && rq[0].id == rk[0].id && rq[0].start == qi * kTile &&
+      rq[0].stop == (qi + 1) * kTile && rk[0].start == kj * kTile &&
+      rk[0].stop == (kj + 1) * kTile && (!causal || kj < qi))
+    return 2;
+  return 1;
 }
 
-// One wave per query-tile row (work list of k tiles) or key-tile column
-// (work list of q tiles), compacted in increasing tile order.
-__global__ __launch_bounds__(64) void worklist_kernel(MapArgs a) {
+// One block per query-tile row (tile map row and work list of k tiles) or
+// key-tile column (work list of q tiles): the row's or column's pairs are
+// classified one per thread, and the non-empty ones are compacted in
+// increasing tile order as `tile * 4 + class` (ballots within each wave, a
+// prefix over the block's waves through LDS).  Column blocks classify their
+// pairs again rather than waiting for the row blocks' map.
+constexpr int kListThreads = 256;
+
+__global__ __launch_bounds__(kListThreads) void tile_lists_kernel(MapArgs a) {
+  __shared__ int wave_n[kListThreads / 64];
   const int b = blockIdx.y;
   const int t = blockIdx.x;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nq = a.lay.nq, nk = a.lay.nk;
-  const uint8_t* tmap = reinterpret_cast<const uint8_t*>(a.plan + a.lay.tmap) + (size_t)b * nq * nk;
+  uint8_t* tmap = reinterpret_cast<uint8_t*>(a.plan + a.lay.tmap) + (size_t)b * nq * nk;
   const bool row = t < nq;
   const int fixed = row ? t : t - nq;
   const int len = row ? nk : nq;
@@ -185,16 +187,28 @@ __global__ __launch_bounds__(64) void worklist_kernel(MapArgs a) {
   int* count = row ? plan_i32(a.plan, a.lay.qcnt) + (size_t)b * nq + fixed
                    : plan_i32(a.plan, a.lay.kcnt) + (size_t)b * nk + fixed;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int n = 0;
-  for (int base = 0; base < len; base += 64) {
-    const int i = base + lane;
+  int n = 0;  // entries written by earlier rounds (same value in every thread)
+  for (int base = 0; base < len; base += kListThreads) {
+    const int i = base + threadIdx.x;
     int cls = 0;
-    if (i < len) cls = row ? tmap[(size_t)fixed * nk + i] : tmap[(size_t)i * nk + fixed];
+    if (i < len) {
+      cls = row ? pair_class(a, b, fixed, i) : pair_class(a, b, i, fixed);
+      if (row) tmap[(size_t)fixed * nk + i] = (uint8_t)cls;
+    }
     const uint64_t bits = __ballot(cls != 0);
-    if (cls != 0) list[n + __popcll(bits & below)] = i * 4 + cls;
-    n += __popcll(bits);
+    if (lane == 0) wave_n[wave] = __popcll(bits);
+    __syncthreads();
+    int before = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kListThreads / 64; ++w) {
+      before += w < wave ? wave_n[w] : 0;
+      total += wave_n[w];
+    }
+    if (cls != 0) list[n + before + __popcll(bits & below)] = i * 4 + cls;
+    n += total;
+    __syncthreads();  // wave_n is rewritten by the next round
   }
-  if (lane == 0) *count = n;
+  if (threadIdx.x == 0) *count = n;
 }
 
 // Launch orders for the attention grids: the (row, tile) items sorted by
@@ -284,9 +298,8 @@ __global__ __launch_bounds__(256) void placement_ids_kernel(MapArgs a, const int
 
 static void launch_map_tail(const MapArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(tile_runs_kernel, dim3(a.lay.nq + a.lay.nk, a.batch), dim3(64), 0, stream, a);
-  hipLaunchKernelGGL(classify_kernel, dim3((a.lay.nq * a.lay.nk + 255) / 256, a.batch), dim3(256),
-                     0, stream, a);
-  hipLaunchKernelGGL(worklist_kernel, dim3(a.lay.nq + a.lay.nk, a.batch), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL(tile_lists_kernel, dim3(a.lay.nq + a.lay.nk, a.batch), dim3(kListThreads), 0,
+                     stream, a);
   hipLaunchKernelGGL(order_kernel, dim3(2), dim3(kOrderThreads), 0, stream, a);
 }
 
