@@ -128,11 +128,12 @@ def test_bidirectional_packed_fixture(device):
 
 @pytest.mark.parametrize("mode", [0, 1, 2])
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
-def test_random_layouts_against_oracle(mode, dtype, device):
+@pytest.mark.parametrize("t", [333, 517])
+def test_random_layouts_against_oracle(mode, dtype, t, device):
     """Ragged T, non-contiguous ids, masked holes, GQA 2; FP64 oracle."""
-    rng = np.random.default_rng(40 + mode)
-    b, t, hq, hkv = 2, 333, 4, 2
-    s = 200 if mode == 2 else t
+    rng = np.random.default_rng(40 + mode + t)
+    b, hq, hkv = 2, 4, 2
+    s = (200 if t == 333 else 611) if mode == 2 else t
     say("random layout", mode, dtype, (b, t, s))
     q, k, v, do = operands(rng, b, t, hq, hkv, 64, DT[dtype], 0.5, s=s)
     if mode == 2:
@@ -158,19 +159,30 @@ def test_random_layouts_against_oracle(mode, dtype, device):
             assert bf16_scaled_error(a.cpu(), torch.tensor(r)) < BF16_TOL, name
 
 
-@pytest.mark.parametrize("hq, hkv", [(4, 4), (8, 2), (6, 2), (3, 1)])
-def test_gqa_ratios(hq, hkv, device):
+@pytest.mark.parametrize("hq, hkv", [(4, 4), (8, 2), (6, 2), (3, 1), (16, 2), (2, 2)])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_gqa_ratios(hq, hkv, dtype, mode, device):
+    """Every query-head group size the launchers dispatch on (G = 1, 3, 4, 8 next to the
+    G = 2 of the other tests): one head per wave, head pairs, odd groups."""
     rng = np.random.default_rng(hq * 10 + hkv)
     b, t = 1, 256
-    say("gqa", hq, hkv)
-    q, k, v, do = operands(rng, b, t, hq, hkv, 64, torch.float32, 0.5)
+    say("gqa", hq, hkv, dtype, "mode", mode)
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, DT[dtype], 0.5)
     seg = np.repeat([[1, 2, 3, 0]], [100, 90, 50, 16], axis=1).astype(np.int32)
     ts = torch.tensor(seg, device=device)
-    got = _grads(lambda a, bb, c: bidirectional.attention(a, bb, c, ts != 0, ts), q, k, v, do)
-    ref = oatt.grouped_fp64(1, *(x.cpu().numpy() for x in (q, k, v)), seg != 0, seg,
-                            d_out=do.cpu().numpy())
-    for a, r in zip(got, ref):
-        np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5)
+    if mode == 0:
+        fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, ts != 0, ts)  # noqa: E731
+    else:
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, ts != 0, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = oatt.grouped_fp64(mode, *(x.float().cpu().numpy() for x in (q, k, v)), seg != 0, seg,
+                            d_out=do.float().cpu().numpy())
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        if dtype == "float32":
+            np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
+        else:
+            assert bf16_scaled_error(a.cpu(), torch.tensor(r)) < BF16_TOL, name
 
 
 @pytest.mark.parametrize("name", ["C2", "C3", "C5"])
