@@ -93,18 +93,24 @@ def test_scalar_length_broadcasts_and_backends_agree(device):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_decode_step_appends_per_row(dtype, device):
+@pytest.mark.parametrize("dtype,hq,hkv", [
+    (torch.float32, 8, 2),
+    (torch.bfloat16, 8, 2),   # the streaming kernel appends (G = 4)
+    (torch.bfloat16, 2, 2),   # G = 1
+    (torch.bfloat16, 16, 2),  # G = 8
+    (torch.bfloat16, 6, 2),   # G = 3: the prep kernel appends, the LDS-staged kernel decodes
+])
+def test_decode_step_appends_per_row(dtype, hq, hkv, device):
     """Ragged KV-cache append + decode (layers/attention.py:309-317, one slot per row).
 
     Slots follow dynamic_update_slice's start clamping to [0, capacity - 1];
     the step attends over position + 1 slots (position >= capacity reads every
     slot, a negative position gives the uniform average, as mf_decode)."""
     rng = np.random.default_rng(9)
-    cap, hq, hkv = 300, 8, 2
+    cap = 300
     positions = np.array([0, 1, 150, 255, 256, 299, 300, 1000, -1], np.int32)
     b = positions.size
-    say("decode append", dtype, positions.tolist())
+    say("decode append", dtype, "hq", hq, "hkv", hkv, positions.tolist())
     t = lambda x: torch.tensor(x, device=device).to(dtype)  # noqa: E731
     q, kn, vn = (t(rng.standard_normal(s).astype(np.float32))
                  for s in ((b, 1, hq, 64), (b, 1, hkv, 64), (b, 1, hkv, 64)))
