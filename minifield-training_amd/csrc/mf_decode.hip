@@ -533,14 +533,21 @@ __global__ __launch_bounds__(512) void decode_bf16_kernel(DecArgs a) {
   }
 }
 
-// One wave per (row, query head).  The chunk maxima and sums are combined
-// lane-parallel over chunks; the outputs with lane = d, loading the chunks'
-// partial outputs independently of each other.
+// One block of kCombineWaves waves per (row, query head).  Every wave
+// combines the chunk maxima and sums lane-parallel over chunks (the same
+// values in every wave); wave w then accumulates the weighted partial outputs
+// of chunks w, w + kCombineWaves, ... with lane = d, and the waves' sums are
+// added in wave order through LDS.  Splitting the chunks over waves shortens
+// the chain of dependent loads each lane waits on.
+constexpr int kCombineWaves = 4;
+
 template <bool F32>
-__global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
+__global__ __launch_bounds__(64 * kCombineWaves) void decode_combine_kernel(DecArgs a) {
+  __shared__ float part[kCombineWaves][kD];
   const int bh = blockIdx.x;
   const int b = bh / a.Hq;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
   const int nch = (eff_len(raw_length(a.lengths, a.positions, b), a.cap) + a.chunk - 1) / a.chunk;
   const float* src = a.partial + (size_t)bh * a.maxc * (2 + kD);
   float M = kNegInf;
@@ -552,9 +559,15 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecArgs a) {
   L = wave_sum(L);
   float acc = 0.f;
 #pragma unroll 4
-  for (int ch = 0; ch < nch; ++ch)
+  for (int ch = wave; ch < nch; ch += kCombineWaves)
     acc = fmaf(src[ch * (2 + kD) + 2 + lane], fast_exp2(src[ch * (2 + kD)] - M), acc);
-  const float o = acc / L;
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < kCombineWaves; ++w) total += part[w][lane];
+  const float o = total / L;
   if constexpr (!F32) reinterpret_cast<bf16*>(a.out)[(size_t)bh * kD + lane] = (bf16)o;
   else reinterpret_cast<float*>(a.out)[(size_t)bh * kD + lane] = o;
 }
@@ -612,7 +625,8 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
   if (gx < 1) gx = 1;
   if (f32) {
     hipLaunchKernelGGL((decode_kernel<true>), dim3(gx, Hkv), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL((decode_combine_kernel<true>), dim3(batch * Hq), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((decode_combine_kernel<true>), dim3(batch * Hq), dim3(64 * kCombineWaves), 0,
+                       stream, a);
     return hipGetLastError();
   }
   // bf16: persistent grid of 4-wave blocks over (chunk item, KV head)
@@ -626,7 +640,8 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
     case 8: hipLaunchKernelGGL((decode_bf16_kernel<8>), dim3(blocks), dim3(256), 0, stream, a); break;
     default: hipLaunchKernelGGL((decode_kernel<false>), dim3(gx, Hkv), dim3(256), 0, stream, a); break;
   }
-  hipLaunchKernelGGL((decode_combine_kernel<false>), dim3(batch * Hq), dim3(64), 0, stream, a);
+  hipLaunchKernelGGL((decode_combine_kernel<false>), dim3(batch * Hq), dim3(64 * kCombineWaves), 0,
+                     stream, a);
   return hipGetLastError();
 }
 
