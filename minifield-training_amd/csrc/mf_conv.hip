@@ -81,8 +81,9 @@ __device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
 // product with (1, 1).
 template <typename T, int K>
 __global__ __launch_bounds__(256) void segmented_conv_kernel(ConvArgs a) {
-  // inputs in flight ahead of the one in use (2-7 KB per wave), chosen so
-  // that lcm(K, kAhead) stays small enough to unroll
+  // input tokens whose v, b and c loads are in flight ahead of the one in use
+  // (fewer for fp32, whose rows are twice as wide), chosen so that
+  // lcm(K, kAhead) stays small enough to unroll
   constexpr int kAhead = std::is_same<T, float>::value ? 2 : (K <= 4 || K == 8) ? 4 : K;
   constexpr int kIn = kConvTile + K - 1;
   constexpr bool kBf16 = !std::is_same<T, float>::value;
