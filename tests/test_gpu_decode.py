@@ -148,3 +148,35 @@ def test_decode_step_scalar_position_and_small_head_dim(device):
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
     with pytest.raises(ValueError, match="Unsupported cached attention backend"):
         attention.cached_attention_step(q, kn, vn, kc, vc, 5, backend="splash")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_incremental_decode_equals_the_causal_forward(dtype, device):
+    """Token-by-token decode with per-row appends equals the packed causal
+    forward over the whole sequence, at every position (the invariant of
+    tests/layers/test_blocks.py:223-291: incremental decoding reproduces the
+    uninterrupted pass).  Ties the decode path to the forward path: two
+    different kernel families computing the same rows."""
+    rng = np.random.default_rng(12)
+    b, n, cap, hq, hkv = 3, 80, 96, 8, 2
+    say("incremental decode", dtype, (b, n, cap))
+    t = lambda x: torch.tensor(x, device=device).to(dtype)  # noqa: E731
+    q, k, v = (t(rng.standard_normal((b, n, h, 64)).astype(np.float32) * 0.5) for h in (hq, hkv, hkv))
+    ones = torch.ones(b, n, dtype=torch.int32, device=device)
+    full = attention.dense_packed_causal_attention(q, k, v, ones, ones)
+    kc = torch.zeros(b, cap, hkv, 64, dtype=dtype, device=device)
+    vc = torch.zeros_like(kc)
+    steps = []
+    for i in range(n):
+        pos = torch.full((b,), i, dtype=torch.int32, device=device)
+        out, kc, vc = attention.cached_attention_step(q[:, i:i + 1], k[:, i:i + 1], v[:, i:i + 1],
+                                                      kc, vc, pos)
+        steps.append(out)
+    inc = torch.cat(steps, dim=1)
+    assert torch.equal(kc[:, :n], k) and torch.equal(vc[:, :n], v)
+    if dtype == torch.float32:
+        np.testing.assert_allclose(inc.cpu().numpy(), full.cpu().numpy(), rtol=1e-5, atol=1e-5)
+    else:
+        # both round P to bf16 at different points (the decode's split-K
+        # partials against the forward's 32-key blocks)
+        assert max_abs(inc.float(), full.float()) < 2e-2
