@@ -459,9 +459,8 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     return s;
   };
 
-  // masks (ids and/or causal), online softmax, O += P V for one block
-  auto softmax_pv = [&](f32x16& s, const char* vt, const int* kids_lds, int kb, int kb2,
-                        bool mask_ids, bool diag) {
+  // masks and shifted scores of one block; returns its row max (both halves)
+  auto prep_block = [&](f32x16& s, const int* kids_lds, int kb, int kb2, bool mask_ids, bool diag) {
     if (mask_ids) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
@@ -484,24 +483,10 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     float mx = fmaxf(s[0], s[1]);
 #pragma unroll
     for (int r = 2; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[r]), s[r + 1]);
-    mx = halves_max(mx);
-    const bool grow = mx > lag;
-    if (__any(grow)) {
-      // a growing lane moves its shift to the new max: d > 0 and finite, so
-      // alpha = 2^-d is finite (a lane with no valid key yet has l = 0, O = 0)
-      const float d = grow ? mx : 0.f;
-      const float alpha = fast_exp2(-d);
-      shift += d;
-      lag = grow ? 8.f : lag;
-      l0 *= alpha;
-      l1 *= alpha;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        oacc[0][r] *= alpha;
-        oacc[1][r] *= alpha;
-        s[r] -= d;
-      }
-    }
+    return mx;
+  };
+  // exponentials, row sums and O += P V of one block
+  auto finish_pv = [&](f32x16& s, const char* vt, int kb2) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = fast_exp2(s[r]);
     const bf16x8 p0 = pack8(s, 0), p1 = pack8(s, 8);
@@ -527,9 +512,10 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     }
   };
 
-  // One step = two 32-key blocks.  Both score blocks are issued before the
-  // softmax of the first, so the second block's MFMAs run under that VALU
-  // work (and the first block's P V under the second block's softmax).
+  // One step = two 32-key blocks.  Both score blocks are issued before any
+  // softmax work, so the second block's MFMAs run under the first block's
+  // masks and max; both blocks share one shift decision; the first block's
+  // P V then runs under the second block's exponentials.
   auto compute = [&](int step, const char* stage) {
     const int entry = ld_const(list, step >> 1);
     const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
@@ -557,8 +543,36 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     f32x16 s0, s1;
     if (run[0]) s0 = scores(kt, 0);
     if (run[1]) s1 = scores(kt, 1);
-    if (run[0]) softmax_pv(s0, vt, kids_lds, kb, 0, mask_ids[0], diag[0]);
-    if (run[1]) softmax_pv(s1, vt, kids_lds, kb, 1, mask_ids[1], diag[1]);
+    // One shift decision for the step's two blocks, taken before either
+    // block's probabilities exist.  A growing lane moves its shift to the new
+    // max: d > 0 and finite, so alpha = 2^-d is finite (a lane with no valid
+    // key yet has l = 0, O = 0).
+    float mx = kNegInf;
+    if (run[0]) mx = prep_block(s0, kids_lds, kb, 0, mask_ids[0], diag[0]);
+    if (run[1]) mx = fmaxf(mx, prep_block(s1, kids_lds, kb, 1, mask_ids[1], diag[1]));
+    mx = halves_max(mx);
+    const bool grow = mx > lag;
+    if (__any(grow)) {
+      const float d = grow ? mx : 0.f;
+      const float alpha = fast_exp2(-d);
+      shift += d;
+      lag = grow ? 8.f : lag;
+      l0 *= alpha;
+      l1 *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        oacc[0][r] *= alpha;
+        oacc[1][r] *= alpha;
+      }
+      if (run[0])
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s0[r] -= d;
+      if (run[1])
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s1[r] -= d;
+    }
+    if (run[0]) finish_pv(s0, vt, 0);
+    if (run[1]) finish_pv(s1, vt, 1);
   };
 
   // Ring of two 128-key slots: the DMAs of slot i+1 are issued right after
