@@ -390,15 +390,20 @@ def cpu_leg(seconds: float):
 # profiles/traffic.json, which the timed run reports as roofline.traffic.
 # --------------------------------------------------------------------------
 CALIB_BYTES = 512 << 20
-TRAFFIC_KERNELS = {  # bench name -> device kernels (name prefixes, any template arguments)
-    "block_map": ("mf::token_ids_kernel", "mf::tile_runs_kernel", "mf::tile_lists_kernel",
-                  "mf::order_kernel"),
-    "attn_fwd": ("mf::attn_fwd_bf16_kernel<",),
-    "attn_bwd_dq": ("mf::bwd_dq_bf16_kernel<",),  # computes D itself in the product call
-    "attn_bwd_dkdv": ("mf::bwd_dkdv_bf16_kernel<",),
-    "decode": ("mf::decode_prep_kernel", "mf::decode_bf16_kernel<", "mf::decode_combine_kernel<"),
-    "qk_norm_rope": ("mf::qk_norm_rope_kernel<",),
-    "segmented_conv": ("mf::segmented_conv_kernel<",),
+TRAFFIC_KERNELS = {
+    # bench name -> (device kernels as name prefixes, workload, which dispatch of each kernel:
+    # None = the mean over the run's dispatches; 0 / 1 = the first / second, for kernels that
+    # --profile-step launches for two different calls)
+    "block_map": (("mf::token_ids_kernel", "mf::tile_runs_kernel", "mf::tile_lists_kernel",
+                   "mf::order_kernel"), "C2", None),
+    "attn_fwd": (("mf::attn_fwd_bf16_kernel<",), "C2", None),
+    "attn_bwd_dq": (("mf::bwd_dq_bf16_kernel<",), "C2", None),  # computes D itself in the product call
+    "attn_bwd_dkdv": (("mf::bwd_dkdv_bf16_kernel<",), "C2", None),
+    "decode": (("mf::decode_prep_kernel", "mf::decode_bf16_kernel<", "mf::decode_combine_kernel<"),
+               "C4", 0),
+    "decode_append": (("mf::decode_bf16_kernel<", "mf::decode_combine_kernel<"), "C4", 1),
+    "qk_norm_rope": (("mf::qk_norm_rope_kernel<",), "C2", None),
+    "segmented_conv": (("mf::segmented_conv_kernel<",), "C2", None),
 }
 
 
@@ -415,39 +420,45 @@ def profile_step() -> None:
     rows_leg(0, profile=True)
 
 
-def _counter_means(path: pathlib.Path) -> dict:
+def _counter_values(path: pathlib.Path) -> dict:
+    """Counter value per dispatch, grouped by kernel name in dispatch order."""
     import csv
     import re
 
-    sums, counts = {}, {}
+    sums = {}
     for row in csv.DictReader(open(path)):
         name = re.sub(r"\(.*", "", row["Kernel_Name"]).replace("void ", "").strip()
         mangled = re.match(r"_ZN2mf(\d+)", name)  # left mangled when a template argument is __bf16
         if mangled:
             name = "mf::" + name[mangled.end():mangled.end() + int(mangled.group(1))] + "<"
-        key = (name, int(row.get("Dispatch_Id", 0) or 0))
+        key = (int(row.get("Dispatch_Id", 0) or 0), name)
         sums[key] = sums.get(key, 0.0) + float(row["Counter_Value"])
     per_kernel = {}
-    for (name, _), value in sums.items():
+    for (_, name), value in sorted(sums.items()):
         per_kernel.setdefault(name, []).append(value)
-    return {name: sum(v) / len(v) for name, v in per_kernel.items()} | {
-        "__calls__": {name: len(v) for name, v in per_kernel.items()}}
+    return per_kernel
 
 
 def traffic_from(fetch_dir: str, write_dir: str) -> dict:
-    fetch = _counter_means(next(pathlib.Path(fetch_dir).rglob("*counter_collection.csv")))
-    write = _counter_means(next(pathlib.Path(write_dir).rglob("*counter_collection.csv")))
+    fetch = _counter_values(next(pathlib.Path(fetch_dir).rglob("*counter_collection.csv")))
+    write = _counter_values(next(pathlib.Path(write_dir).rglob("*counter_collection.csv")))
     copy = "__amd_rocclr_copyBuffer"
-    calls_f, calls_w = fetch["__calls__"].get(copy, 1), write["__calls__"].get(copy, 1)
-    f_scale = CALIB_BYTES / (fetch[copy] * calls_f * 1024)
-    w_scale = CALIB_BYTES / (write[copy] * calls_w * 1024)
-    out = {"calibration": {"copy_bytes": CALIB_BYTES, "fetch_kib_per_copy": fetch[copy] * calls_f,
-                           "write_kib_per_copy": write[copy] * calls_w,
+    f_scale = CALIB_BYTES / (sum(fetch[copy]) * 1024)
+    w_scale = CALIB_BYTES / (sum(write[copy]) * 1024)
+    out = {"calibration": {"copy_bytes": CALIB_BYTES, "fetch_kib_per_copy": sum(fetch[copy]),
+                           "write_kib_per_copy": sum(write[copy]),
                            "fetch_scale": f_scale, "write_scale": w_scale}}
-    for name, kernels in TRAFFIC_KERNELS.items():
-        fb = sum(v for k, v in fetch.items() if k.startswith(kernels)) * 1024 * f_scale
-        wb = sum(v for k, v in write.items() if k.startswith(kernels)) * 1024 * w_scale
-        workload = "C4" if name == "decode" else "C2"
+
+    def per_launch(values: dict, kernels, occurrence):
+        total = 0.0
+        for name, v in values.items():
+            if name.startswith(kernels):
+                total += v[occurrence] if occurrence is not None else sum(v) / len(v)
+        return total
+
+    for name, (kernels, workload, occurrence) in TRAFFIC_KERNELS.items():
+        fb = per_launch(fetch, kernels, occurrence) * 1024 * f_scale
+        wb = per_launch(write, kernels, occurrence) * 1024 * w_scale
         out.setdefault(workload, {})[name] = {"fetch_bytes": fb, "write_bytes": wb,
                                               "bytes": fb + wb}
     (ROOT / "profiles").mkdir(exist_ok=True)
