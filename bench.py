@@ -25,6 +25,10 @@
   probabilities; fwd + autograd bwd), timed per (row, KV-group) chunk of the
   same C2 batch for about ``--cpu-seconds`` and scaled to useful TFLOP/s.
 
+``--config C3`` or ``--config C5`` times the same step on the causal packed
+workloads instead (C3: 4 x 8192, mean segment 512; C5: 1 x 32768, segments of
+16-128 tokens) and prints the step's line alone.
+
 Only one GPU is used; ``--gpus`` above 1 exits with a message.
 """
 
@@ -74,14 +78,14 @@ def _traffic(kernel: str, workload: str):
     return None if entry is None else entry["bytes"]
 
 
-def gpu_leg(steps: int, warmup: int, profile: bool = False):
+def gpu_leg(steps: int, warmup: int, profile: bool = False, name: str = "C2", decode: bool = True):
     import numpy as np
     import torch
 
     from mfattn import _lib, ops, workloads
 
     dev = torch.device("cuda:0")
-    w = workloads.packed("C2")
+    w = workloads.packed(name)
     mode = _lib.MODE_PACKED_CAUSAL if w.causal else _lib.MODE_PACKED_BIDIR
     rng = np.random.default_rng(w.seed)
 
@@ -165,7 +169,7 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False):
         "roofline": {"bound": "mfma", "kernel": dominant, "achieved": achieved,
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-                     "traffic": _traffic(dominant, "C2"),
+                     "traffic": _traffic(dominant, name),
                      "algorithmic_gflop_per_launch": algo[dominant] / 1e9},
         "fa2_convention_tflops": flops["fwd_bwd_fa2"] / (ms * 1e-3) / 1e12,
         "step_roofline_frac": (flops["fwd_bwd"] / (MFMA_BF16_PEAK_TFLOPS * 1e12)) / (ms * 1e-3),
@@ -173,7 +177,7 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False):
     }
     del q, k, v, do, dq, dk, dv, out, lse, plan, ws
     torch.cuda.empty_cache()
-    result["decode"] = decode_leg(steps, warmup)
+    result["decode"] = decode_leg(steps, warmup) if decode else None
     return result
 
 
@@ -476,6 +480,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", default="C2", choices=("C2", "C3", "C5"),
+                    help="packed workload of the step (C2, the default, is the headline line with "
+                         "the decode, the rows and the CPU baseline; C3 and C5 print the step alone)")
     ap.add_argument("--profile-step", action="store_true",
                     help="run the calibration copy, one C2 step, one C4 decode and the rows once "
                          "(for rocprofv3 --pmc)")
@@ -492,6 +499,15 @@ def main() -> int:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
               "(the packed-attention path has no cross-GPU work in this build)", file=sys.stderr)
         return 2
+    if args.config != "C2":
+        gpu = gpu_leg(args.steps, args.warmup, name=args.config, decode=False)
+        print(json.dumps({"metric": METRIC.split(";")[0], "value": gpu["value"], "unit": "TFLOP/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": gpu["ms_per_step"], "higher_is_better": True,
+                          "dtype": "bf16", "config": gpu["config"], "roofline": gpu["roofline"],
+                          "kernels_ms": gpu["kernels_ms"],
+                          "step_roofline_frac": gpu["step_roofline_frac"]}))
+        return 0
     gpu = gpu_leg(args.steps, args.warmup)
     line = {
         "metric": METRIC,
