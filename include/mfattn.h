@@ -191,6 +191,24 @@ int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain,
                     int head_dim, float eps, float rope_theta, void* q_out,
                     void* k_out, void* stream);
 
+/* Backward of mf_qk_norm_rope (the VJP JAX autodiff derives for the
+ * reference's rms_norm + apply_rotary, kernels/normalization.py:7-22,
+ * kernels/rotary.py:7-39, as layers/attention.py:62-97 composes them):
+ * given dq_out / dk_out (the gradients of q_out / k_out), writes dq / dk in
+ * the tensor dtype and the gain gradients dq_gain / dk_gain ([64] fp32,
+ * summed over every token and head in a fixed order: deterministic).  Inputs
+ * and positions as for the forward call; dq / dk may alias dq_out / dk_out.
+ * `workspace` holds per-workgroup gain partials
+ * (mf_qk_norm_rope_bwd_workspace_bytes). */
+size_t mf_qk_norm_rope_bwd_workspace_bytes(int batch, int seq_len);
+int mf_qk_norm_rope_bwd(const void* q, const void* k, const void* q_gain,
+                        const void* k_gain, const int32_t* positions,
+                        const void* dq_out, const void* dk_out, int dtype,
+                        int batch, int seq_len, int q_heads, int kv_heads,
+                        int head_dim, float eps, float rope_theta, void* dq,
+                        void* dk, float* dq_gain, float* dk_gain,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Per-token positions from segment ids on the device: the offset of each
  * token inside its run of equal nonzero ids, 0 for padding -- the positions
  * batching/packing.py:92-100 builds on the host for packed rows. */
@@ -213,6 +231,24 @@ int mf_segmented_conv(const void* b_gate, const void* c_gate, const void* values
                       const void* taps, const int32_t* segment_ids, int mode,
                       int dtype, int batch, int seq_len, int channels,
                       int kernel_size, void* out, void* stream);
+
+/* Backward of mf_segmented_conv (the VJP JAX autodiff derives for
+ * kernels/bidirectional.py:38-58 and kernels/convolution.py:25-53 with the
+ * gate products of models/lfm2_5/encoder.py:80-85): given d_out, writes
+ * d_values, d_b_gate and d_c_gate in the tensor dtype (each gate gradient
+ * only when that gate is given; pass NULL for both or neither) and the tap
+ * gradients d_taps ([channels, kernel_size] fp32, summed over rows and tokens
+ * in a fixed order: deterministic).  `workspace` holds per-workgroup tap
+ * partials (mf_segmented_conv_bwd_workspace_bytes). */
+size_t mf_segmented_conv_bwd_workspace_bytes(int batch, int seq_len,
+                                             int channels, int kernel_size);
+int mf_segmented_conv_bwd(const void* b_gate, const void* c_gate,
+                          const void* values, const void* taps,
+                          const int32_t* segment_ids, const void* d_out,
+                          int mode, int dtype, int batch, int seq_len,
+                          int channels, int kernel_size, void* d_b_gate,
+                          void* d_c_gate, void* d_values, float* d_taps,
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* mf_last_error(void);

@@ -30,6 +30,13 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* q_gain,
                                const void* k_gain, const int32_t* positions, bool f32, int B,
                                int T, int Hq, int Hkv, float eps, float theta, void* q_out,
                                void* k_out, hipStream_t stream);
+size_t rope_bwd_workspace_bytes(int B, int T);
+hipError_t launch_qk_norm_rope_bwd(const void* q, const void* k, const void* q_gain,
+                                   const void* k_gain, const int32_t* positions,
+                                   const void* dq_out, const void* dk_out, bool f32, int B, int T,
+                                   int Hq, int Hkv, float eps, float theta, void* dq, void* dk,
+                                   float* dq_gain, float* dk_gain, void* workspace,
+                                   hipStream_t stream);
 hipError_t launch_segment_positions(const int32_t* seg, int B, int T, int32_t* pos,
                                     hipStream_t stream);
 hipError_t launch_block_map_placements(const int32_t* placements, int count, int mode, int batch,
@@ -38,6 +45,11 @@ hipError_t launch_block_map_placements(const int32_t* placements, int count, int
 hipError_t launch_segmented_conv(const void* b, const void* c, const void* v, const void* w,
                                  const int32_t* seg, bool centered, bool f32, int B, int T, int C,
                                  int K, void* out, hipStream_t stream);
+size_t conv_bwd_workspace_bytes(int B, int T, int C, int K);
+hipError_t launch_segmented_conv_bwd(const void* b, const void* c, const void* v, const void* w,
+                                     const int32_t* seg, const void* g, bool centered, bool f32,
+                                     int B, int T, int C, int K, void* db, void* dc, void* dv,
+                                     float* dw, void* workspace, hipStream_t stream);
 }  // namespace mf
 
 namespace {
@@ -99,6 +111,7 @@ int check_attn(int dtype, int batch, int q_len, int kv_len, int q_heads, int kv_
 }
 
 }  // namespace
+
 
 extern "C" {
 
@@ -260,8 +273,8 @@ size_t mf_decode_workspace_bytes(int batch, int capacity, int q_heads, int head_
 
 namespace {
 
-int check_decode(int dtype, int batch, int capacity, int q_heads, int kv_heads, int head_dim,
-                 size_t workspace_bytes) {
+int check_decode_shape(int dtype, int batch, int capacity, int q_heads, int kv_heads,
+                       int head_dim) {
   if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
     return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
   if (batch < 1 || capacity < 1 || q_heads < 1 || kv_heads < 1)
@@ -274,6 +287,12 @@ int check_decode(int dtype, int batch, int capacity, int q_heads, int kv_heads, 
   if (q_heads / kv_heads > 8)
     return fail(MF_ERR_HEADS, "Decode serves at most 8 query heads per KV head (got %d)",
                 q_heads / kv_heads);
+  return MF_OK;
+}
+
+int check_decode(int dtype, int batch, int capacity, int q_heads, int kv_heads, int head_dim,
+                 size_t workspace_bytes) {
+  if (int rc = check_decode_shape(dtype, batch, capacity, q_heads, kv_heads, head_dim)) return rc;
   const size_t need = mf_decode_workspace_bytes(batch, capacity, q_heads, head_dim);
   if (workspace_bytes < need)
     return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
@@ -299,33 +318,21 @@ int mf_decode_append(const void* q, const void* k_new, const void* v_new,
 int mf_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* lengths,
               int dtype, int batch, int capacity, int q_heads, int kv_heads, int head_dim,
               float scale, void* out, void* workspace, size_t workspace_bytes, void* stream) {
-  if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
-    return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
-  if (batch < 1 || capacity < 1 || q_heads < 1 || kv_heads < 1)
-    return fail(MF_ERR_INVALID_ARGUMENT,
-                "Sizes must be positive (batch=%d capacity=%d q_heads=%d kv_heads=%d)", batch,
-                capacity, q_heads, kv_heads);
-  if (head_dim != mf::kD)
-    return fail(MF_ERR_SHAPE, "Cached attention query/KV shapes are incompatible");
-  if (q_heads % kv_heads) return fail(MF_ERR_HEADS, "Query heads must be divisible by KV heads");
-  if (q_heads / kv_heads > 8)
-    return fail(MF_ERR_HEADS, "Decode serves at most 8 query heads per KV head (got %d)",
-                q_heads / kv_heads);
+  if (int rc = check_decode_shape(dtype, batch, capacity, q_heads, kv_heads, head_dim)) return rc;
   if (!q || !k_cache || !v_cache || !lengths || !out || !workspace)
     return fail(MF_ERR_INVALID_ARGUMENT, "every tensor pointer and the workspace must be non-null");
-  const size_t need = mf_decode_workspace_bytes(batch, capacity, q_heads, head_dim);
-  if (workspace_bytes < need)
-    return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  if (int rc = check_decode(dtype, batch, capacity, q_heads, kv_heads, head_dim, workspace_bytes))
+    return rc;
   return check_hip(mf::launch_decode(q, k_cache, v_cache, lengths, dtype == MF_DTYPE_F32, batch,
                                      capacity, q_heads, kv_heads, scale, out, workspace,
                                      static_cast<hipStream_t>(stream)),
                    "mf_decode launch");
 }
 
-int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain, const void* k_gain,
-                    const int32_t* positions, int dtype, int batch, int seq_len, int q_heads,
-                    int kv_heads, int head_dim, float eps, float rope_theta, void* q_out,
-                    void* k_out, void* stream) {
+namespace {
+
+int check_rope(int dtype, int batch, int seq_len, int q_heads, int kv_heads, int head_dim,
+               float rope_theta) {
   if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
     return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
   if (batch < 1 || seq_len < 1 || q_heads < 1 || kv_heads < 1)
@@ -334,13 +341,51 @@ int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain, const void
                 seq_len, q_heads, kv_heads);
   if (head_dim != mf::kD)
     return fail(MF_ERR_HEAD_DIM, "head_dim must be %d (got %d)", mf::kD, head_dim);
+  if (!(rope_theta > 0.f)) return fail(MF_ERR_INVALID_ARGUMENT, "rope_theta must be positive");
+  return MF_OK;
+}
+
+}  // namespace
+
+int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain, const void* k_gain,
+                    const int32_t* positions, int dtype, int batch, int seq_len, int q_heads,
+                    int kv_heads, int head_dim, float eps, float rope_theta, void* q_out,
+                    void* k_out, void* stream) {
+  if (int rc = check_rope(dtype, batch, seq_len, q_heads, kv_heads, head_dim, rope_theta))
+    return rc;
   if (!q || !k || !q_gain || !k_gain || !q_out || !k_out)
     return fail(MF_ERR_INVALID_ARGUMENT, "a required tensor pointer is null");
-  if (!(rope_theta > 0.f)) return fail(MF_ERR_INVALID_ARGUMENT, "rope_theta must be positive");
   return check_hip(mf::launch_qk_norm_rope(q, k, q_gain, k_gain, positions, dtype == MF_DTYPE_F32,
                                            batch, seq_len, q_heads, kv_heads, eps, rope_theta,
                                            q_out, k_out, static_cast<hipStream_t>(stream)),
                    "mf_qk_norm_rope launch");
+}
+
+size_t mf_qk_norm_rope_bwd_workspace_bytes(int batch, int seq_len) {
+  if (batch < 1 || seq_len < 1) return 0;
+  return mf::rope_bwd_workspace_bytes(batch, seq_len);
+}
+
+int mf_qk_norm_rope_bwd(const void* q, const void* k, const void* q_gain, const void* k_gain,
+                        const int32_t* positions, const void* dq_out, const void* dk_out,
+                        int dtype, int batch, int seq_len, int q_heads, int kv_heads,
+                        int head_dim, float eps, float rope_theta, void* dq, void* dk,
+                        float* dq_gain, float* dk_gain, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  if (int rc = check_rope(dtype, batch, seq_len, q_heads, kv_heads, head_dim, rope_theta))
+    return rc;
+  if (!q || !k || !q_gain || !k_gain || !dq_out || !dk_out || !dq || !dk || !dq_gain ||
+      !dk_gain || !workspace)
+    return fail(MF_ERR_INVALID_ARGUMENT, "a required tensor pointer or the workspace is null");
+  const size_t need = mf_qk_norm_rope_bwd_workspace_bytes(batch, seq_len);
+  if (workspace_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  return check_hip(mf::launch_qk_norm_rope_bwd(q, k, q_gain, k_gain, positions, dq_out, dk_out,
+                                               dtype == MF_DTYPE_F32, batch, seq_len, q_heads,
+                                               kv_heads, eps, rope_theta, dq, dk, dq_gain,
+                                               dk_gain, workspace,
+                                               static_cast<hipStream_t>(stream)),
+                   "mf_qk_norm_rope_bwd launch");
 }
 
 int mf_segment_positions(const int32_t* segment_ids, int batch, int seq_len, int32_t* positions,
@@ -355,10 +400,9 @@ int mf_segment_positions(const int32_t* segment_ids, int batch, int seq_len, int
                    "mf_segment_positions launch");
 }
 
-int mf_segmented_conv(const void* b_gate, const void* c_gate, const void* values,
-                      const void* taps, const int32_t* segment_ids, int mode, int dtype,
-                      int batch, int seq_len, int channels, int kernel_size, void* out,
-                      void* stream) {
+namespace {
+
+int check_conv(int mode, int dtype, int batch, int seq_len, int channels, int kernel_size) {
   if (dtype != MF_DTYPE_F32 && dtype != MF_DTYPE_BF16)
     return fail(MF_ERR_DTYPE, "Unsupported dtype code %d", dtype);
   if (mode != MF_CONV_CAUSAL && mode != MF_CONV_CENTERED)
@@ -370,6 +414,16 @@ int mf_segmented_conv(const void* b_gate, const void* c_gate, const void* values
     return fail(MF_ERR_SHAPE, "channels must be a multiple of 8 (got %d)", channels);
   if (kernel_size < 1 || kernel_size > 8)
     return fail(MF_ERR_SHAPE, "kernel_size must be in [1, 8] (got %d)", kernel_size);
+  return MF_OK;
+}
+
+}  // namespace
+
+int mf_segmented_conv(const void* b_gate, const void* c_gate, const void* values,
+                      const void* taps, const int32_t* segment_ids, int mode, int dtype,
+                      int batch, int seq_len, int channels, int kernel_size, void* out,
+                      void* stream) {
+  if (int rc = check_conv(mode, dtype, batch, seq_len, channels, kernel_size)) return rc;
   if (!values || !taps || !out)
     return fail(MF_ERR_INVALID_ARGUMENT, "values, taps and out must be non-null");
   return check_hip(mf::launch_segmented_conv(b_gate, c_gate, values, taps, segment_ids,
@@ -379,8 +433,59 @@ int mf_segmented_conv(const void* b_gate, const void* c_gate, const void* values
                    "mf_segmented_conv launch");
 }
 
+size_t mf_segmented_conv_bwd_workspace_bytes(int batch, int seq_len, int channels,
+                                             int kernel_size) {
+  if (batch < 1 || seq_len < 1 || channels < 1 || kernel_size < 1) return 0;
+  return mf::conv_bwd_workspace_bytes(batch, seq_len, channels, kernel_size);
+}
+
+int mf_segmented_conv_bwd(const void* b_gate, const void* c_gate, const void* values,
+                          const void* taps, const int32_t* segment_ids, const void* d_out,
+                          int mode, int dtype, int batch, int seq_len, int channels,
+                          int kernel_size, void* d_b_gate, void* d_c_gate, void* d_values,
+                          float* d_taps, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_conv(mode, dtype, batch, seq_len, channels, kernel_size)) return rc;
+  if (!values || !taps || !d_out || !d_values || !d_taps || !workspace)
+    return fail(MF_ERR_INVALID_ARGUMENT,
+                "values, taps, d_out, d_values, d_taps and the workspace must be non-null");
+  if ((b_gate == nullptr) != (d_b_gate == nullptr) || (c_gate == nullptr) != (d_c_gate == nullptr))
+    return fail(MF_ERR_INVALID_ARGUMENT,
+                "a gate and its gradient must both be given or both be null");
+  const size_t need = mf_segmented_conv_bwd_workspace_bytes(batch, seq_len, channels, kernel_size);
+  if (workspace_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "workspace holds %zu bytes, %zu needed", workspace_bytes, need);
+  return check_hip(mf::launch_segmented_conv_bwd(b_gate, c_gate, values, taps, segment_ids, d_out,
+                                                 mode == MF_CONV_CENTERED, dtype == MF_DTYPE_F32,
+                                                 batch, seq_len, channels, kernel_size, d_b_gate,
+                                                 d_c_gate, d_values, d_taps, workspace,
+                                                 static_cast<hipStream_t>(stream)),
+                   "mf_segmented_conv_bwd launch");
+}
+
 const char* mf_last_error(void) { return g_last_error.c_str(); }
 
 const char* mf_version(void) { return "mfattn 0.1.0 (gfx950)"; }
 
 }  // extern "C"
+
+// Validation and error reporting shared with the other C-ABI source files.
+namespace mf {
+
+int abi_fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int abi_check_hip(hipError_t e, const char* what) { return check_hip(e, what); }
+
+int abi_check_decode_shape(int dtype, int batch, int capacity, int q_heads, int kv_heads,
+                           int head_dim) {
+  return check_decode_shape(dtype, batch, capacity, q_heads, kv_heads, head_dim);
+}
+
+}  // namespace mf

@@ -75,6 +75,16 @@ __device__ __forceinline__ float halves_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// x rounded to bf16 (nearest even) and widened back to fp32.  The conversion
+// is inline asm so that no floating-point rewrite can drop it: written as
+// (float)(bf16)x, the compiler has fused a product rounded this way into a
+// following add (one FMA, the rounding gone).
+__device__ __forceinline__ float round_bf16(float x) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, 0" : "=v"(r) : "v"(x));
+  return __builtin_bit_cast(float, r << 16);
+}
+
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane j receives
 // element e (0..3) = halfword (j & 3) of the 8 bytes addressed by lane
 // (j >> 2) + 4e.  If lane i of the group addresses row base + (i >> 2),

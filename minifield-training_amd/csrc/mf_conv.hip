@@ -9,9 +9,11 @@
 // segment ids: 0 <= s < T, the zero padding of the unsegmented versions).
 // b and c may be absent (1).  Depthwise: channel c uses taps w[c, :].
 //
-// dtype contract: b*v, every tap product and c*mixed are rounded to the
-// tensor dtype as in the reference; the tap sum accumulates in fp32 and is
-// rounded once.  [B, T, C] row-major, C a multiple of 8.
+// dtype contract: b*v, every tap product, every partial tap sum (in tap
+// order) and c*mixed are rounded to the tensor dtype, the reference's
+// declared dtypes (bidirectional.py:48-57, convolution.py:41-52), so the bf16
+// result is the reference's bit for bit.  [B, T, C] row-major, C a multiple
+// of 8.
 //
 // Thread = (row, 8 channels, 32 consecutive output tokens): a sliding window
 // of the K gated inputs lives in registers, so every input element is read
@@ -66,11 +68,6 @@ __device__ __forceinline__ uint32_t round_pair(float x, float y, float& rx, floa
 
 constexpr int conv_gcd(int x, int y) { return y ? conv_gcd(y, x % y) : x; }
 
-// acc + lo + hi of a packed bf16 pair (products with 1 are exact).
-__device__ __forceinline__ float dot2_ones(uint32_t pair, float acc) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair),
-                                         __builtin_bit_cast(bf16x2, 0x3F803F80u), acc, false);
-}
 
 // Thread = (row, 8 channels, kConvTile consecutive output tokens).  Input
 // token u of the tile (u = 0 .. kConvTile + K - 2, token t0 + lo + u) is
@@ -162,36 +159,30 @@ __global__ __launch_bounds__(256) void segmented_conv_kernel(ConvArgs a) {
       const int me = sid[win(ctr)];
       const size_t off = (row + t0 + j) * a.C + c0;  // output element
       if constexpr (kBf16) {
-        // taps in pairs (2p, 2p + 1): both rounded products packed by one
-        // conversion, the halves of taps outside the token's segment masked
-        // off, and the pair added to the fp32 sum by a dot product with (1, 1)
-        constexpr int kPairs = (K + 1) / 2;
-        uint32_t keep[kPairs];
+        // the reference's declared-dtype order: each tap product rounded, the
+        // taps added one at a time in tap order with every partial sum
+        // rounded (taps outside the token's segment add an exact zero); two
+        // channels share each conversion
+        bool on[K];
 #pragma unroll
-        for (int q = 0; q < kPairs; ++q) {
-          const bool on0 = me != 0 && sid[win(2 * q)] == me;
-          const bool on1 = 2 * q + 1 < K && me != 0 && sid[win(2 * q + 1)] == me;
-          keep[q] = (on0 ? 0x0000ffffu : 0u) | (on1 ? 0xffff0000u : 0u);
-        }
+        for (int i = 0; i < K; ++i) on[i] = me != 0 && sid[win(i)] == me;
         uint32_t words[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-          float sum[2];
+          float m0 = 0.f, m1 = 0.f;
 #pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            float acc = 0.f;
-#pragma unroll
-            for (int q = 0; q < kPairs; ++q) {
-              const float p0 = g[win(2 * q)][e + h] * w[2 * q][e + h];
-              const float p1 = 2 * q + 1 < K ? g[win(2 * q + 1)][e + h] * w[2 * q + 1][e + h] : 0.f;
-              acc = dot2_ones(pack_pair(p0, p1) & keep[q], acc);
+          for (int i = 0; i < K; ++i) {
+            float p0, p1;
+            round_pair(g[win(i)][e] * w[i][e], g[win(i)][e + 1] * w[i][e + 1], p0, p1);
+            if (!on[i]) p0 = p1 = 0.f;
+            if (i == 0) {
+              m0 = p0;
+              m1 = p1;
+            } else {
+              round_pair(m0 + p0, m1 + p1, m0, m1);
             }
-            sum[h] = acc;
           }
-          float m0, m1;
-          uint32_t word = round_pair(sum[0], sum[1], m0, m1);
-          if (a.c) word = pack_pair(cu[e] * m0, cu[e + 1] * m1);
-          words[e / 2] = word;
+          words[e / 2] = a.c ? pack_pair(cu[e] * m0, cu[e + 1] * m1) : pack_pair(m0, m1);
         }
         const u32x4 x = {words[0], words[1], words[2], words[3]};
         *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(a.out) + off) = x;
@@ -216,6 +207,268 @@ __global__ __launch_bounds__(256) void segmented_conv_kernel(ConvArgs a) {
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Backward (the VJP of out[t] = c[t] * m[t], m[t] = sum_i u[t + o_i] w_i
+// keep(t, t + o_i), u = b * v, o_i = lo + i).  With h = g * c:
+//   dc[t] = g[t] * m[t]
+//   du[s] = sum_i h[s - o_i] w_i keep(s - o_i, s)     (keep is symmetric)
+//   db = du * v,  dv = du * b,  dw_i = sum_{b,t} h[t] u[t + o_i] keep(t, t + o_i)
+// in fp32 from the tensor-dtype operands (u and m rounded as the forward
+// rounds them), each gradient rounded once.  Thread = (row, 8 channels, 32
+// output tokens); a workgroup holds 8 channel chunks x 32 token tiles, so the
+// tap-gradient terms of its 32 tiles are added inside it (lanes, then waves)
+// and written as one partial per (workgroup row, channel, tap); a second
+// launch adds the partials in order (deterministic, no atomics).  Neighbour
+// tokens are re-read through the cache, not from HBM: a thread's loads walk
+// 32 + K - 1 consecutive token rows.
+// ---------------------------------------------------------------------------
+struct ConvBwdArgs {
+  const void* b;
+  const void* c;
+  const void* v;
+  const void* w;
+  const int32_t* seg;
+  const void* g;   // d out
+  void* db;
+  void* dc;
+  void* dv;
+  float* partials;  // [B * tile groups][C][K]
+  int B, T, C, K, centered;
+};
+
+constexpr int kConvBwdTiles = 32;   // token tiles per workgroup
+constexpr int kConvBwdChunks = 8;   // 8-channel chunks per workgroup
+
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&x)[8]) {
+  Raw8<T> r;
+  r.load(p);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = r[e];
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&x)[8]) {
+  if constexpr (std::is_same<T, float>::value) {
+    f32x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) lo[e] = x[e], hi[e] = x[4 + e];
+    *reinterpret_cast<f32x4*>(p) = lo;
+    *reinterpret_cast<f32x4*>(p + 4) = hi;
+  } else {
+    uint32_t words[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) words[e / 2] = pack_pair(x[e], x[e + 1]);
+    const u32x4 v = {words[0], words[1], words[2], words[3]};
+    *reinterpret_cast<u32x4*>(p) = v;
+  }
+}
+
+template <typename T, int K>
+__global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) {
+  constexpr bool kBf16 = !std::is_same<T, float>::value;
+  __shared__ float red[4][kConvBwdChunks][K * 8];
+  const int chunks = a.C / 8;
+  const int tiles = (a.T + kConvTile - 1) / kConvTile;
+  const int cgroups = (chunks + kConvBwdChunks - 1) / kConvBwdChunks;
+  const int tgroups = (tiles + kConvBwdTiles - 1) / kConvBwdTiles;
+  const int cg = blockIdx.x % cgroups;
+  const int tg = (blockIdx.x / cgroups) % tgroups;
+  const int b = blockIdx.x / (cgroups * tgroups);
+  const int lc = threadIdx.x % kConvBwdChunks, lt = threadIdx.x / kConvBwdChunks;
+  const int ch = cg * kConvBwdChunks + lc;
+  const int tile = tg * kConvBwdTiles + lt;
+  const bool on = ch < chunks && tile < tiles;
+  const int c0 = min(ch, chunks - 1) * 8;
+  const int lo = a.centered ? -(K / 2) : -(K - 1);
+  const size_t row = (size_t)b * a.T;
+  const T* vp = reinterpret_cast<const T*>(a.v);
+  const T* bp = reinterpret_cast<const T*>(a.b);
+  const T* cp = reinterpret_cast<const T*>(a.c);
+  const T* gp = reinterpret_cast<const T*>(a.g);
+
+  float w[K][8];
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[i][e] = (float)reinterpret_cast<const T*>(a.w)[(size_t)(c0 + e) * K + i];
+  float dw[K][8];
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dw[i][e] = 0.f;
+
+  auto seg_of = [&](int s) { return (s < 0 || s >= a.T) ? 0 : a.seg ? a.seg[row + s] : 1; };
+  // u = b * v at token s (rounded as the forward rounds it), 0 outside the row
+  auto load_u = [&](int s, float (&u)[8]) {
+    const int sc = min(max(s, 0), a.T - 1);
+    load8<T>(vp + (row + sc) * a.C + c0, u);
+    if (a.b) {
+      float bb[8];
+      load8<T>(bp + (row + sc) * a.C + c0, bb);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) u[e] = kBf16 ? round_bf16(u[e] * bb[e]) : u[e] * bb[e];
+    }
+  };
+  // h = g * c at token s
+  auto load_h = [&](int s, float (&h)[8]) {
+    const int sc = min(max(s, 0), a.T - 1);
+    load8<T>(gp + (row + sc) * a.C + c0, h);
+    if (a.c) {
+      float cc[8];
+      load8<T>(cp + (row + sc) * a.C + c0, cc);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] *= cc[e];
+    }
+  };
+
+  if (on) {
+    const int t0 = tile * kConvTile;
+    const int tend = min(t0 + kConvTile, a.T);
+    for (int t = t0; t < tend; ++t) {
+      const int me = seg_of(t);
+      const size_t off = (row + t) * a.C + c0;
+      float h[8], m[8], du[8];
+      load_h(t, h);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) m[e] = 0.f, du[e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        // forward tap: u at t + o_i feeds m[t] (rounded in tap order as the
+        // forward does); transposed tap: h at t - o_i feeds du[t]
+        const int s_fwd = t + lo + i, s_bwd = t - lo - i;
+        const bool keep_fwd = me != 0 && seg_of(s_fwd) == me;
+        const bool keep_bwd = me != 0 && seg_of(s_bwd) == me;
+        if (keep_fwd) {
+          float u[8];
+          load_u(s_fwd, u);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float p = u[e] * w[i][e];
+            m[e] = kBf16 ? round_bf16(round_bf16(p) + m[e]) : m[e] + p;
+            dw[i][e] = fmaf(h[e], u[e], dw[i][e]);
+          }
+        }
+        if (keep_bwd) {
+          float hn[8];
+          load_h(s_bwd, hn);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) du[e] = fmaf(hn[e], w[i][e], du[e]);
+        }
+      }
+      if (a.dc) {
+        float gg[8], dc[8];
+        load8<T>(gp + off, gg);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dc[e] = gg[e] * m[e];
+        store8<T>(reinterpret_cast<T*>(a.dc) + off, dc);
+      }
+      float vv[8], dv[8];
+      if (a.b) {
+        float bb[8], db[8];
+        load8<T>(bp + off, bb);
+        load8<T>(vp + off, vv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dv[e] = du[e] * bb[e], db[e] = du[e] * vv[e];
+        store8<T>(reinterpret_cast<T*>(a.db) + off, db);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dv[e] = du[e];
+      }
+      store8<T>(reinterpret_cast<T*>(a.dv) + off, dv);
+    }
+  }
+  // tap gradients: add the 8 tiles of each wave (lanes lc, lc + 8, ... hold
+  // the same channels), then the 4 waves, in a fixed order
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = dw[i][e];
+      x += __shfl_xor(x, 8);
+      x += __shfl_xor(x, 16);
+      x += __shfl_xor(x, 32);
+      if (lane < kConvBwdChunks) red[wave][lane][i * 8 + e] = x;
+    }
+  __syncthreads();
+  for (int j = threadIdx.x; j < kConvBwdChunks * K * 8; j += blockDim.x) {
+    const int jc = j / (K * 8), ie = j % (K * 8), i = ie / 8, e = ie % 8;
+    const int chj = cg * kConvBwdChunks + jc;
+    if (chj >= chunks) continue;
+    const float x = ((red[0][jc][ie] + red[1][jc][ie]) + red[2][jc][ie]) + red[3][jc][ie];
+    a.partials[((size_t)(b * tgroups + tg) * a.C + chj * 8 + e) * K + i] = x;
+  }
+}
+
+// d taps [C][K] fp32: the partials of every (row, tile group) added in order.
+__global__ __launch_bounds__(256) void conv_taps_reduce_kernel(const float* partials, int parts,
+                                                               int n, float* dw) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  float acc = 0.f;
+  for (int p = 0; p < parts; ++p) acc += partials[(size_t)p * n + j];
+  dw[j] = acc;
+}
+
+size_t conv_bwd_parts(int B, int T) {
+  const int tiles = (T + kConvTile - 1) / kConvTile;
+  return (size_t)B * ((tiles + kConvBwdTiles - 1) / kConvBwdTiles);
+}
+
+size_t conv_bwd_workspace_bytes(int B, int T, int C, int K) {
+  return conv_bwd_parts(B, T) * (size_t)C * K * sizeof(float);
+}
+
+template <typename T>
+hipError_t launch_conv_bwd_t(const ConvBwdArgs& a, hipStream_t stream) {
+  const int chunks = a.C / 8;
+  const int tiles = (a.T + kConvTile - 1) / kConvTile;
+  const long long blocks = (long long)a.B * ((tiles + kConvBwdTiles - 1) / kConvBwdTiles) *
+                           ((chunks + kConvBwdChunks - 1) / kConvBwdChunks);
+  const dim3 grid((unsigned)blocks);
+  switch (a.K) {
+    case 1: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 1>), grid, dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 2>), grid, dim3(256), 0, stream, a); break;
+    case 3: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 3>), grid, dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
+    case 5: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 5>), grid, dim3(256), 0, stream, a); break;
+    case 6: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 6>), grid, dim3(256), 0, stream, a); break;
+    case 7: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 7>), grid, dim3(256), 0, stream, a); break;
+    case 8: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 8>), grid, dim3(256), 0, stream, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_segmented_conv_bwd(const void* b, const void* c, const void* v, const void* w,
+                                     const int32_t* seg, const void* g, bool centered, bool f32,
+                                     int B, int T, int C, int K, void* db, void* dc, void* dv,
+                                     float* dw, void* workspace, hipStream_t stream) {
+  ConvBwdArgs a;
+  a.b = b;
+  a.c = c;
+  a.v = v;
+  a.w = w;
+  a.seg = seg;
+  a.g = g;
+  a.db = db;
+  a.dc = dc;
+  a.dv = dv;
+  a.partials = static_cast<float*>(workspace);
+  a.B = B;
+  a.T = T;
+  a.C = C;
+  a.K = K;
+  a.centered = centered;
+  const hipError_t e = f32 ? launch_conv_bwd_t<float>(a, stream) : launch_conv_bwd_t<bf16>(a, stream);
+  if (e != hipSuccess) return e;
+  const int n = C * K;
+  hipLaunchKernelGGL(conv_taps_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                     a.partials, (int)conv_bwd_parts(B, T), n, dw);
+  return hipGetLastError();
 }
 
 template <typename T>

@@ -9,9 +9,10 @@
 //   out = n * dtype(cos(a)) + rotate_half(n) * dtype(sin(a)),
 //   a_i = f32(position) * f32(theta^(-2i/D)),  rotate_half(n) = (-n[D/2:], n[:D/2])
 // with the frequencies computed on the host (single precision, as the
-// reference).  In bf16 the products with the gain and the rotation are
-// rounded once each (the final combination at fp32, as XLA's fused
-// elementwise code does).
+// reference).  In bf16 every operation rounds to bf16 as the reference's
+// declared dtypes do (its tests pin them with xla_allow_excess_precision
+// off): the normalised value, its product with the gain, cos and sin, the
+// two rotation products and their sum.
 //
 // Layout: one wave per token.  Lanes 0..31 compute the token's 32 angles'
 // cos/sin into LDS; then lane (g = lane / 8, dl = lane % 8) owns dims
@@ -19,6 +20,7 @@
 // two 16-byte (fp32) loads per lane move 8 whole head rows, the sum of
 // squares reduces over 8 lanes with DPP, and the rotation partner (dims
 // +- 32) is lane dl ^ 4 of the same head.
+#include <algorithm>
 #include <type_traits>
 
 #include "mf_common.h"
@@ -59,8 +61,8 @@ __device__ __forceinline__ void norm_rope_rows(const void* src, void* dst, const
     c[i] = cs[d & 31];
     s[i] = sn[d & 31];
     if constexpr (!F32) {
-      c[i] = (float)(bf16)c[i];
-      s[i] = (float)(bf16)s[i];
+      c[i] = round_bf16(c[i]);
+      s[i] = round_bf16(s[i]);
     }
   }
   for (int h0 = 0; h0 < H; h0 += 8) {
@@ -86,9 +88,9 @@ __device__ __forceinline__ void norm_rope_rows(const void* src, void* dst, const
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float v = x[i] * inv;
-      if constexpr (!F32) v = (float)(bf16)v;
+      if constexpr (!F32) v = round_bf16(v);
       v *= w[i];
-      if constexpr (!F32) v = (float)(bf16)v;
+      if constexpr (!F32) v = round_bf16(v);
       n[i] = v;
     }
     // rotate_half: dims d < 32 take -n[d + 32], dims d >= 32 take n[d - 32]
@@ -110,9 +112,25 @@ __device__ __forceinline__ void norm_rope_rows(const void* src, void* dst, const
     } else {
       bf16x8 o;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (bf16)fmaf(n[i], c[i], r[i] * s[i]);
+      for (int i = 0; i < 8; ++i)
+        o[i] = (bf16)(round_bf16(n[i] * c[i]) + round_bf16(r[i] * s[i]));
       *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(dst) + base) = o;
     }
+  }
+}
+
+// cos and sin of the token's 32 angles f32(position) * freq[i] into LDS
+// (lanes 0..31), shared by the forward and the backward so both use the
+// same values.
+__device__ __forceinline__ void token_angles(const int32_t* positions, size_t tok, int T,
+                                             const float* freq, int lane, float* cs, float* sn) {
+  const int t = (int)(tok % T);
+  const float pos = (float)(positions ? positions[tok] : t);
+  if (lane < kD / 2) {
+    float sv, cv;
+    sincosf(pos * freq[lane], &sv, &cv);
+    cs[lane] = cv;
+    sn[lane] = sv;
   }
 }
 
@@ -124,18 +142,177 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   const size_t token = (size_t)blockIdx.x * 4 + wave;  // b * T + t
   const size_t total = (size_t)a.B * a.T;
   const size_t tok = token < total ? token : total - 1;  // tail waves redo the last token, no store
-  const int t = (int)(tok % a.T);
-  const float pos = (float)(a.positions ? a.positions[tok] : t);
-  if (lane < kD / 2) {
-    float sv, cv;
-    sincosf(pos * a.freq[lane], &sv, &cv);
-    cs_l[wave][lane] = cv;
-    sn_l[wave][lane] = sv;
-  }
+  token_angles(a.positions, tok, a.T, a.freq, lane, cs_l[wave], sn_l[wave]);
   __syncthreads();
   if (token >= total) return;
   norm_rope_rows<F32>(a.q, a.q_out, a.q_gain, a.Hq, tok, lane, cs_l[wave], sn_l[wave], a.eps);
   norm_rope_rows<F32>(a.k, a.k_out, a.k_gain, a.Hkv, tok, lane, cs_l[wave], sn_l[wave], a.eps);
+}
+
+// ---------------------------------------------------------------------------
+// Backward (the VJP JAX autodiff derives for the reference's prologue).  Per
+// head row, with y = x * inv, inv = rsqrt(mean(x^2) + eps), n = y * w and
+// out = n * C + rot(n) * S:
+//   dn_j = g_j C_j + (j < 32 ? g_{j+32} : -g_{j-32}) S_j      (rot^T)
+//   dw  += dn * y   (y as the forward rounded it: y cast to the dtype)
+//   dy   = dn * w
+//   dx   = inv * (dy - y * mean(dy * y))
+// everything in fp32 from the tensor-dtype operands, dx rounded once.  The
+// gain gradients sum over every token and head: each wave accumulates its
+// tokens' terms in registers, the workgroup adds its four waves, and a second
+// launch adds the per-workgroup partials in workgroup order (deterministic,
+// no atomics).
+// ---------------------------------------------------------------------------
+struct RopeBwdArgs {
+  const void* q;
+  const void* k;
+  const void* q_gain;
+  const void* k_gain;
+  const int32_t* positions;
+  const void* dq_out;
+  const void* dk_out;
+  void* dq;
+  void* dk;
+  float* partials;  // [gridDim.x][2][64]
+  int B, T, Hq, Hkv;
+  float eps;
+  float freq[kD / 2];
+};
+
+constexpr int kRopeBwdBlocks = 1024;  // workgroups of the backward (fewer for short inputs)
+
+template <bool F32>
+__device__ __forceinline__ void norm_rope_rows_bwd(const void* src, const void* gout, void* dst,
+                                                   const void* gain, int H, size_t token,
+                                                   int lane, const float* cs, const float* sn,
+                                                   float eps, float (&dw)[8]) {
+  typedef typename std::conditional<F32, float, bf16>::type T;
+  const int g = lane >> 3, dl = lane & 7;
+  float w[8], c[8], s[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int d = 8 * dl + i;
+    w[i] = (float)reinterpret_cast<const T*>(gain)[d];
+    c[i] = cs[d & 31];
+    s[i] = sn[d & 31];
+    if constexpr (!F32) {
+      c[i] = round_bf16(c[i]);
+      s[i] = round_bf16(s[i]);
+    }
+  }
+  for (int h0 = 0; h0 < H; h0 += 8) {
+    const int h = h0 + g;
+    const bool live = h < H;
+    const size_t base = (token * H + min(h, H - 1)) * kD + 8 * dl;
+    float x[8], go[8];
+    if constexpr (F32) {
+      const float* xs = reinterpret_cast<const float*>(src) + base;
+      const float* gs = reinterpret_cast<const float*>(gout) + base;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(xs);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(xs + 4);
+      const f32x4 ga = *reinterpret_cast<const f32x4*>(gs);
+      const f32x4 gb = *reinterpret_cast<const f32x4*>(gs + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i], go[i] = ga[i], go[4 + i] = gb[i];
+    } else {
+      const bf16x8 a = ld_bf16x8(reinterpret_cast<const bf16*>(src) + base);
+      const bf16x8 ga = ld_bf16x8(reinterpret_cast<const bf16*>(gout) + base);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) x[i] = (float)a[i], go[i] = (float)ga[i];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+    const float inv = rsqrtf(dpp_xor_sum8(ss) * (1.f / kD) + eps);
+    float dy[8], y[8], dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // rot^T: dims d < 32 take +g[d + 32], dims d >= 32 take -g[d - 32]
+      const float o = __shfl_xor(go[i], 4);
+      const float dn = fmaf(go[i], c[i], (dl < 4 ? o : -o) * s[i]);
+      y[i] = x[i] * inv;
+      const float yr = F32 ? y[i] : round_bf16(y[i]);
+      if (live) dw[i] = fmaf(dn, yr, dw[i]);
+      dy[i] = dn * w[i];
+      dot = fmaf(dy[i], y[i], dot);
+    }
+    const float mean = dpp_xor_sum8(dot) * (1.f / kD);
+    if (!live) continue;
+    if constexpr (F32) {
+      f32x4 a, b;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = inv * fmaf(-y[i], mean, dy[i]);
+        b[i] = inv * fmaf(-y[4 + i], mean, dy[4 + i]);
+      }
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base) = a;
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base + 4) = b;
+    } else {
+      bf16x8 o;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = (bf16)(inv * fmaf(-y[i], mean, dy[i]));
+      *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(dst) + base) = o;
+    }
+  }
+}
+
+// Sum of x over the 8 lanes l, l ^ 8, ..., l ^ 56 (the 8 heads of a group
+// that hold the same dims).
+__device__ __forceinline__ float heads_sum8(float x) {
+  x += __shfl_xor(x, 8);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+template <bool F32>
+__global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(RopeBwdArgs a) {
+  __shared__ float cs_l[4][kD / 2], sn_l[4][kD / 2];
+  __shared__ float part[4][2][kD];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const size_t total = (size_t)a.B * a.T;
+  const size_t stride = (size_t)gridDim.x * 4;
+  float dwq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dwk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  // every wave runs the same number of iterations (tokens past the end redo
+  // the last token and store nothing), so the block-wide barriers match
+  const size_t iters = (total + stride - 1) / stride;
+  for (size_t it = 0; it < iters; ++it) {
+    const size_t token = it * stride + (size_t)blockIdx.x * 4 + wave;
+    const size_t tok = token < total ? token : total - 1;
+    __syncthreads();  // the previous token's angles have been read
+    token_angles(a.positions, tok, a.T, a.freq, lane, cs_l[wave], sn_l[wave]);
+    __syncthreads();
+    if (token >= total) continue;
+    norm_rope_rows_bwd<F32>(a.q, a.dq_out, a.dq, a.q_gain, a.Hq, tok, lane, cs_l[wave],
+                            sn_l[wave], a.eps, dwq);
+    norm_rope_rows_bwd<F32>(a.k, a.dk_out, a.dk, a.k_gain, a.Hkv, tok, lane, cs_l[wave],
+                            sn_l[wave], a.eps, dwk);
+  }
+  const int dl = lane & 7;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float sq = heads_sum8(dwq[i]), sk = heads_sum8(dwk[i]);
+    if (lane < 8) {
+      part[wave][0][8 * dl + i] = sq;
+      part[wave][1][8 * dl + i] = sk;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 2 * kD) {
+    const int which = threadIdx.x / kD, d = threadIdx.x % kD;
+    const float v = ((part[0][which][d] + part[1][which][d]) + part[2][which][d]) + part[3][which][d];
+    a.partials[((size_t)blockIdx.x * 2 + which) * kD + d] = v;
+  }
+}
+
+// dq_gain / dk_gain: the per-workgroup partials added in workgroup order.
+__global__ __launch_bounds__(128) void rope_gain_reduce_kernel(const float* partials, int blocks,
+                                                               float* dq_gain, float* dk_gain) {
+  const int which = threadIdx.x / kD, d = threadIdx.x % kD;
+  float acc = 0.f;
+  for (int b = 0; b < blocks; ++b) acc += partials[((size_t)b * 2 + which) * kD + d];
+  (which ? dk_gain : dq_gain)[d] = acc;
 }
 
 // Packer positions from segment ids: the offset of each token inside its run
@@ -197,6 +374,48 @@ hipError_t launch_qk_norm_rope(const void* q, const void* k, const void* q_gain,
     hipLaunchKernelGGL((qk_norm_rope_kernel<true>), grid, dim3(256), 0, stream, a);
   else
     hipLaunchKernelGGL((qk_norm_rope_kernel<false>), grid, dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+
+size_t rope_bwd_blocks(int B, int T) {
+  const size_t total = (size_t)B * T;
+  return std::min<size_t>((total + 3) / 4, kRopeBwdBlocks);
+}
+
+size_t rope_bwd_workspace_bytes(int B, int T) {
+  return rope_bwd_blocks(B, T) * 2 * kD * sizeof(float);
+}
+
+hipError_t launch_qk_norm_rope_bwd(const void* q, const void* k, const void* q_gain,
+                                   const void* k_gain, const int32_t* positions,
+                                   const void* dq_out, const void* dk_out, bool f32, int B, int T,
+                                   int Hq, int Hkv, float eps, float theta, void* dq, void* dk,
+                                   float* dq_gain, float* dk_gain, void* workspace,
+                                   hipStream_t stream) {
+  RopeBwdArgs a;
+  a.q = q;
+  a.k = k;
+  a.q_gain = q_gain;
+  a.k_gain = k_gain;
+  a.positions = positions;
+  a.dq_out = dq_out;
+  a.dk_out = dk_out;
+  a.dq = dq;
+  a.dk = dk;
+  a.partials = static_cast<float*>(workspace);
+  a.B = B;
+  a.T = T;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.eps = eps;
+  for (int i = 0; i < kD / 2; ++i) a.freq[i] = powf(theta, -((float)(2 * i) / (float)kD));
+  const int blocks = (int)rope_bwd_blocks(B, T);
+  if (f32)
+    hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<true>), dim3(blocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<false>), dim3(blocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL(rope_gain_reduce_kernel, dim3(1), dim3(2 * kD), 0, stream, a.partials,
+                     blocks, dq_gain, dk_gain);
   return hipGetLastError();
 }
 

@@ -53,8 +53,12 @@ EXPORTS = (
     "mf_decode",
     "mf_decode_append",
     "mf_qk_norm_rope",
+    "mf_qk_norm_rope_bwd_workspace_bytes",
+    "mf_qk_norm_rope_bwd",
     "mf_segment_positions",
     "mf_segmented_conv",
+    "mf_segmented_conv_bwd_workspace_bytes",
+    "mf_segmented_conv_bwd",
     "mf_last_error",
     "mf_version",
 )
@@ -115,6 +119,16 @@ def _load() -> ctypes.CDLL:
     lib.mf_qk_norm_rope.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, f32,
                                     vp, vp, vp]
     lib.mf_qk_norm_rope.restype = i32
+    lib.mf_qk_norm_rope_bwd_workspace_bytes.argtypes = [i32, i32]
+    lib.mf_qk_norm_rope_bwd_workspace_bytes.restype = sz
+    lib.mf_qk_norm_rope_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32,
+                                        f32, f32, vp, vp, vp, vp, vp, sz, vp]
+    lib.mf_qk_norm_rope_bwd.restype = i32
+    lib.mf_segmented_conv_bwd_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    lib.mf_segmented_conv_bwd_workspace_bytes.restype = sz
+    lib.mf_segmented_conv_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32,
+                                          vp, vp, vp, vp, vp, sz, vp]
+    lib.mf_segmented_conv_bwd.restype = i32
     lib.mf_segment_positions.argtypes = [vp, i32, i32, vp, vp]
     lib.mf_segment_positions.restype = i32
     lib.mf_block_map_placements.argtypes = [vp, i32, i32, i32, i32, vp, sz, vp, vp, vp]

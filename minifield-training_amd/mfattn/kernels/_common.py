@@ -19,3 +19,16 @@ def fit_head_dim(*xs: torch.Tensor) -> tuple[list[torch.Tensor], int]:
     if 0 < d < _lib.HEAD_DIM:
         return [F.pad(x, (0, _lib.HEAD_DIM - d)) for x in xs], d
     return list(xs), d
+
+
+def promote(*xs: torch.Tensor) -> list[torch.Tensor]:
+    """Cast operands of mixed float dtypes to their common dtype.
+
+    The reference's einsums promote (a float32 query over a bfloat16 cache
+    scores and returns float32, ``attention.py:23-33``); the kernels serve one
+    dtype per call, so mixed operands are cast up front.
+    """
+    dtype = xs[0].dtype
+    for x in xs[1:]:
+        dtype = torch.promote_types(dtype, x.dtype)
+    return [x if x.dtype == dtype else x.to(dtype) for x in xs]

@@ -20,7 +20,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib, ops
-from ._common import fit_head_dim
+from ._common import fit_head_dim, promote
 
 
 def dense_packed_causal_attention(
@@ -29,19 +29,23 @@ def dense_packed_causal_attention(
     value: torch.Tensor,
     attention_mask: torch.Tensor,
     segment_ids: torch.Tensor,
+    *,
+    plan=None,
 ) -> torch.Tensor:
     """Causal attention confined to same-segment active tokens.
 
     A query sees key ``j`` iff ``j <= i``, both share one nonzero segment id
     and both are mask-active (``attention_mask > 0``); inactive query rows are
-    zero.  Output has the query's shape and dtype.
+    zero.  Output has the query's shape and dtype.  ``plan`` (keyword only, not
+    in the reference) is an ``ops.Plan`` built for these ids and this mask in
+    the causal mode; by default one is taken from ``ops.PLANS``.
     """
     # the reference's own (weak) shape check, attention.py:92-93
     if query.shape != key.shape and key.shape != value.shape:
         raise ValueError("Packed attention query/KV shapes are incompatible")
-    (q, k, v), d = fit_head_dim(query, key, value)
+    (q, k, v), d = fit_head_dim(*promote(query, key, value))
     out = ops.packed_attention(q, k, v, attention_mask, segment_ids,
-                               _lib.MODE_PACKED_CAUSAL, d ** -0.5)
+                               _lib.MODE_PACKED_CAUSAL, d ** -0.5, plan)
     return out[..., :d] if out.shape[-1] != d else out
 
 
@@ -61,13 +65,14 @@ def packed_causal_attention(
     segment_ids: torch.Tensor,
     *,
     backend: str,
+    plan=None,
 ) -> torch.Tensor:
     """Apply causal attention confined to same-segment active tokens."""
     try:
         fn = _PACKED_BACKENDS[backend]
     except KeyError:
         raise ValueError(f"Unsupported packed attention backend: {backend}") from None
-    return fn(query, key, value, attention_mask, segment_ids)
+    return fn(query, key, value, attention_mask, segment_ids, plan=plan)
 
 
 def _lengths(valid_length, batch: int, device: torch.device) -> torch.Tensor:
@@ -102,7 +107,8 @@ def dense_cached_attention(
         outs = [dense_cached_attention(query[:, i : i + 1], key, value, valid_length)
                 for i in range(query.shape[1])]
         return torch.cat(outs, dim=1)
-    (q, k, v), d = fit_head_dim(query.contiguous(), key.contiguous(), value.contiguous())
+    (q, k, v), d = fit_head_dim(*promote(query.contiguous(), key.contiguous(),
+                                         value.contiguous()))
     lengths = _lengths(valid_length, query.shape[0], query.device)
     out = ops.decode(q, k, v, lengths, d ** -0.5)
     return out[..., :d] if out.shape[-1] != d else out

@@ -9,7 +9,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib, ops
-from ._common import fit_head_dim
+from ._common import fit_head_dim, promote
 
 
 def attention(
@@ -18,6 +18,8 @@ def attention(
     value: torch.Tensor,
     mask: torch.Tensor,
     segment_ids: torch.Tensor | None = None,
+    *,
+    plan=None,
 ) -> torch.Tensor:
     """Attend in both directions with GQA and zero fully masked rows.
 
@@ -26,9 +28,11 @@ def attention(
     of its own nonzero segment and inactive queries return exact zeros.
     Without them every query of an example sees that example's active keys,
     and examples with no active key return zeros.  ``T`` may differ from
-    ``S`` in the unpacked mode (cross attention).
+    ``S`` in the unpacked mode (cross attention).  ``plan`` (keyword only,
+    not in the reference) is an ``ops.Plan`` built for this mask and these ids;
+    by default one is taken from ``ops.PLANS``.
     """
     mode = _lib.MODE_KEYMASK_BIDIR if segment_ids is None else _lib.MODE_PACKED_BIDIR
-    (q, k, v), d = fit_head_dim(query, key, value)
-    out = ops.packed_attention(q, k, v, mask, segment_ids, mode, d ** -0.5)
+    (q, k, v), d = fit_head_dim(*promote(query, key, value))
+    out = ops.packed_attention(q, k, v, mask, segment_ids, mode, d ** -0.5, plan)
     return out[..., :d] if out.shape[-1] != d else out

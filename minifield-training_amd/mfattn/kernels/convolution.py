@@ -15,26 +15,70 @@ from .. import _lib
 from ..ops import _ptr, _stream, dtype_code, require_device
 
 
+def _launch_forward(bg, cg, v, w, seg, mode, out):
+    b, t, c = v.shape
+    _lib.check(_lib.LIB.mf_segmented_conv(_ptr(bg), _ptr(cg), _ptr(v), _ptr(w), _ptr(seg), mode,
+                                          dtype_code(v), b, t, c, w.shape[1], _ptr(out),
+                                          _stream(v.device)))
+
+
+class SegmentedConv(torch.autograd.Function):
+    """``c * conv(b * v)`` with a HIP forward and a HIP backward (``mf_segmented_conv_bwd``).
+
+    Gradients reach the values, both gates (when given) and the taps; segment
+    ids are integers (no gradient).
+    """
+
+    @staticmethod
+    def forward(ctx, bg, cg, v, w, seg, mode):
+        out = torch.empty_like(v)
+        _launch_forward(bg, cg, v, w, seg, mode, out)
+        ctx.save_for_backward(bg, cg, v, w, seg)
+        ctx.mode = mode
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        bg, cg, v, w, seg = ctx.saved_tensors
+        g = d_out.contiguous()
+        b, t, c = v.shape
+        k = w.shape[1]
+        dv = torch.empty_like(v)
+        db = None if bg is None else torch.empty_like(v)
+        dc = None if cg is None else torch.empty_like(v)
+        dw = torch.empty((c, k), dtype=torch.float32, device=v.device)
+        ws_bytes = _lib.LIB.mf_segmented_conv_bwd_workspace_bytes(b, t, c, k)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=v.device)
+        _lib.check(_lib.LIB.mf_segmented_conv_bwd(
+            _ptr(bg), _ptr(cg), _ptr(v), _ptr(w), _ptr(seg), _ptr(g), ctx.mode, dtype_code(v),
+            b, t, c, k, _ptr(db), _ptr(dc), _ptr(dv), _ptr(dw), _ptr(ws), ws_bytes,
+            _stream(v.device)))
+        return db, dc, dv, dw.to(w.dtype), None, None
+
+
 def _run(b_gate, c_gate, values, taps, segment_ids, mode: int) -> torch.Tensor:
     device = require_device(values)
-    v = values.contiguous()
-    if taps.dim() != 2 or taps.shape[0] != v.shape[-1]:
+    if taps.dim() != 2 or taps.shape[0] != values.shape[-1]:
         raise ValueError("Convolution taps must be [channels, kernel_size]")
+    # the casts below are differentiable: gradients flow back to the callers' dtypes
+    v = values.contiguous()
     w = taps.to(device=device, dtype=v.dtype).contiguous()
     bg = None if b_gate is None else b_gate.to(v.dtype).contiguous()
     cg = None if c_gate is None else c_gate.to(v.dtype).contiguous()
-    for g in (bg, cg):
-        if g is not None and g.shape != v.shape:
+    for gate in (bg, cg):
+        if gate is not None and gate.shape != v.shape:
             raise ValueError("Convolution gates must match the values' shape")
     seg = None if segment_ids is None else segment_ids.to(device=device, dtype=torch.int32).contiguous()
     b, t, c = v.shape
     if seg is not None and tuple(seg.shape) != (b, t):
         raise ValueError("segment_ids must be [batch, tokens]")
-    out = torch.empty_like(v)
-    _lib.check(_lib.LIB.mf_segmented_conv(_ptr(bg), _ptr(cg), _ptr(v), _ptr(w), _ptr(seg), mode,
-                                          dtype_code(v), b, t, c, w.shape[1], _ptr(out),
-                                          _stream(device)))
-    return out
+    needs_grad = torch.is_grad_enabled() and any(
+        x is not None and x.requires_grad for x in (b_gate, c_gate, values, taps))
+    if not needs_grad:
+        out = torch.empty_like(v)
+        _launch_forward(bg, cg, v, w, seg, mode, out)
+        return out
+    return SegmentedConv.apply(bg, cg, v, w, seg, mode)
 
 
 def centered_convolution(gated: torch.Tensor, taps: torch.Tensor,

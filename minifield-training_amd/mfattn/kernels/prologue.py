@@ -33,6 +33,46 @@ def _positions(positions, batch: int, length: int, device: torch.device) -> torc
     return pos.contiguous()
 
 
+def _launch_forward(q, k, qg, kg, pos, eps, theta, q_out, k_out):
+    _lib.check(_lib.LIB.mf_qk_norm_rope(_ptr(q), _ptr(k), _ptr(qg), _ptr(kg), _ptr(pos),
+                                        dtype_code(q), q.shape[0], q.shape[1], q.shape[2],
+                                        k.shape[2], q.shape[3], float(eps), float(theta),
+                                        _ptr(q_out), _ptr(k_out), _stream(q.device)))
+
+
+class QKNormRope(torch.autograd.Function):
+    """The fused prologue with a HIP forward and a HIP backward (``mf_qk_norm_rope_bwd``).
+
+    Gradients reach q, k and both gains; positions are integers (no gradient).
+    """
+
+    @staticmethod
+    def forward(ctx, q, k, qg, kg, pos, eps, theta):
+        q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+        _launch_forward(q, k, qg, kg, pos, eps, theta, q_out, k_out)
+        ctx.save_for_backward(q, k, qg, kg, pos)
+        ctx.eps, ctx.theta = eps, theta
+        return q_out, k_out
+
+    @staticmethod
+    def backward(ctx, dq_out, dk_out):
+        q, k, qg, kg, pos = ctx.saved_tensors
+        dq_out = torch.zeros_like(q) if dq_out is None else dq_out.contiguous()
+        dk_out = torch.zeros_like(k) if dk_out is None else dk_out.contiguous()
+        dq, dk = torch.empty_like(q), torch.empty_like(k)
+        dqg = torch.empty(q.shape[-1], dtype=torch.float32, device=q.device)
+        dkg = torch.empty_like(dqg)
+        b, t = q.shape[:2]
+        ws_bytes = _lib.LIB.mf_qk_norm_rope_bwd_workspace_bytes(b, t)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        _lib.check(_lib.LIB.mf_qk_norm_rope_bwd(
+            _ptr(q), _ptr(k), _ptr(qg), _ptr(kg), _ptr(pos), _ptr(dq_out), _ptr(dk_out),
+            dtype_code(q), b, t, q.shape[2], k.shape[2], q.shape[3], float(ctx.eps),
+            float(ctx.theta), _ptr(dq), _ptr(dk), _ptr(dqg), _ptr(dkg), _ptr(ws), ws_bytes,
+            _stream(q.device)))
+        return dq, dk, dqg.to(qg.dtype), dkg.to(kg.dtype), None, None, None
+
+
 def qk_norm_rope(query: torch.Tensor, key: torch.Tensor, query_gain: torch.Tensor,
                  key_gain: torch.Tensor, positions=None, *, eps: float, rope_theta: float,
                  inplace: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
@@ -40,6 +80,8 @@ def qk_norm_rope(query: torch.Tensor, key: torch.Tensor, query_gain: torch.Tenso
 
     Gains are cast to the tensors' dtype (``weight.astype(x.dtype)`` in the
     reference).  ``positions=None`` means ``0 .. T-1`` on every row.
+    Differentiable in q, k and the gains (HIP backward); ``inplace=True``
+    overwrites q and k and is only allowed when no gradient is being recorded.
     """
     device = require_device(query, key)
     if query.shape[:2] != key.shape[:2] or query.shape[-1] != key.shape[-1] or query.dtype != key.dtype:
@@ -49,13 +91,19 @@ def qk_norm_rope(query: torch.Tensor, key: torch.Tensor, query_gain: torch.Tenso
     q, k = query.contiguous(), key.contiguous()
     qg = query_gain.to(device=device, dtype=query.dtype).contiguous()
     kg = key_gain.to(device=device, dtype=query.dtype).contiguous()
-    q_out = q if inplace else torch.empty_like(q)
-    k_out = k if inplace else torch.empty_like(k)
-    _lib.check(_lib.LIB.mf_qk_norm_rope(_ptr(q), _ptr(k), _ptr(qg), _ptr(kg), _ptr(pos),
-                                        dtype_code(q), b, t, hq, key.shape[2], d, float(eps),
-                                        float(rope_theta), _ptr(q_out), _ptr(k_out),
-                                        _stream(device)))
-    return q_out, k_out
+    needs_grad = torch.is_grad_enabled() and any(
+        x.requires_grad for x in (query, key, query_gain, key_gain))
+    if inplace:
+        if needs_grad:
+            raise ValueError("qk_norm_rope(inplace=True) cannot record gradients; "
+                             "call it out of place or under torch.no_grad()")
+        _launch_forward(q, k, qg, kg, pos, eps, rope_theta, q, k)
+        return q, k
+    if not needs_grad:
+        q_out, k_out = torch.empty_like(q), torch.empty_like(k)
+        _launch_forward(q, k, qg, kg, pos, eps, rope_theta, q_out, k_out)
+        return q_out, k_out
+    return QKNormRope.apply(q, k, qg, kg, pos, float(eps), float(rope_theta))
 
 
 def segment_positions(segment_ids: torch.Tensor) -> torch.Tensor:

@@ -9,6 +9,10 @@ calls the HIP backward once.
 
 from __future__ import annotations
 
+import collections
+import threading
+import weakref
+
 import torch
 
 from . import _lib
@@ -42,6 +46,24 @@ def dtype_code(t: torch.Tensor) -> int:
         return _DTYPES[t.dtype]
     except KeyError:
         raise ValueError(f"Unsupported dtype {t.dtype}; mfattn serves float32 and bfloat16") from None
+
+
+def same_dtype(what: str, *tensors: torch.Tensor) -> int:
+    """The one dtype code every tensor shares; a mix raises before any launch.
+
+    The kernels index every operand with the element size of that one dtype,
+    so a float32 query over a bfloat16 cache would read past the cache.
+    """
+    first = tensors[0].dtype
+    for t in tensors[1:]:
+        if t.dtype != first:
+            raise ValueError(f"{what} must share one dtype (got {first} and {t.dtype})")
+    return dtype_code(tensors[0])
+
+
+def _require_shape(t: torch.Tensor, shape: tuple[int, ...], what: str) -> None:
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{what} must be {list(shape)}, got {list(t.shape)}")
 
 
 def as_mask(mask: torch.Tensor, mode: int) -> tuple[torch.Tensor, int]:
@@ -83,9 +105,22 @@ class Plan:
         return self.section(2, torch.uint8, (self.batch, nq, nk))
 
 
+_BLOCK_MAP_CALLS = [0]  # block-map launches made through this module (plan reuse is tested on it)
+
+
 def block_map(segment_ids: torch.Tensor | None, mask: torch.Tensor, mode: int,
-              q_len: int, kv_len: int) -> Plan:
-    batch = mask.shape[0]
+              q_len: int, kv_len: int, batch: int | None = None) -> Plan:
+    """Build the plan of ``(segment_ids, mask, mode)``.
+
+    ``mask`` must be ``[B, S]`` and ``segment_ids`` ``[B, T]`` exactly: the
+    kernel reads B * S mask entries and B * T ids, and the attention kernels
+    index the plan with the query's batch, so ``batch`` (default
+    ``mask.shape[0]``) is checked against both.
+    """
+    batch = mask.shape[0] if batch is None else batch
+    _require_shape(mask, (batch, kv_len), "mask")
+    if segment_ids is not None:
+        _require_shape(segment_ids, (batch, q_len), "segment_ids")
     device = require_device(mask) if segment_ids is None else require_device(mask, segment_ids)
     m, mcode = as_mask(mask, mode)
     seg = None if segment_ids is None else segment_ids.to(torch.int32).contiguous()
@@ -95,6 +130,7 @@ def block_map(segment_ids: torch.Tensor | None, mask: torch.Tensor, mode: int,
     buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
     _lib.check(_lib.LIB.mf_block_map(_ptr(seg), _ptr(m), mcode, mode, batch, q_len, kv_len,
                                      _ptr(buf), nbytes, _stream(device)))
+    _BLOCK_MAP_CALLS[0] += 1
     return Plan(buf, batch, q_len, kv_len, mode)
 
 
@@ -117,12 +153,31 @@ def block_map_from_placements(placements: torch.Tensor, mode: int, batch: int,
     return Plan(buf, batch, length, length, mode), seg, pos
 
 
+def check_attention_operands(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                             plan: Plan | None = None, mode: int | None = None) -> int:
+    """Shapes, dtypes and plan of one attention call; returns the dtype code.
+
+    ``q [B, T, Hq, D]``, ``k`` and ``v`` ``[B, S, Hkv, D]`` with one dtype; a
+    plan must have been built for the same batch, lengths and mode.
+    """
+    code = same_dtype("query, key and value", q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape or q.shape[0] != k.shape[0] \
+            or q.shape[3] != k.shape[3]:
+        raise ValueError("Packed attention query/KV shapes are incompatible")
+    if plan is not None:
+        if (plan.batch, plan.q_len, plan.kv_len) != (q.shape[0], q.shape[1], k.shape[1]):
+            raise ValueError(
+                f"plan was built for batch {plan.batch}, lengths {plan.q_len}/{plan.kv_len}; "
+                f"the call has {q.shape[0]}, {q.shape[1]}/{k.shape[1]}")
+        if mode is not None and plan.mode != mode:
+            raise ValueError(f"plan was built for mask mode {plan.mode}, the call uses {mode}")
+    return code
+
+
 def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: Plan, mode: int,
              scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    code = check_attention_operands(q, k, v, plan, mode)
     device = require_device(q, k, v)
-    if not (q.dtype == k.dtype == v.dtype):
-        raise ValueError("query, key and value must share one dtype")
-    code = dtype_code(q)
     b, t, hq, d = q.shape
     s, hkv = k.shape[1], k.shape[2]
     out = torch.empty_like(q)
@@ -134,8 +189,11 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: Plan, mode
 
 
 def attn_bwd(q, k, v, out, dout, lse, plan: Plan, mode: int, scale: float):
+    check_attention_operands(q, k, v, plan, mode)
+    code = same_dtype("query, key, value, output and its gradient", q, k, v, out, dout)
+    if out.shape != q.shape or dout.shape != q.shape:
+        raise ValueError("the output and its gradient must have the query's shape")
     device = require_device(q, k, v, out, dout, lse)
-    code = dtype_code(q)
     b, t, hq, d = q.shape
     s, hkv = k.shape[1], k.shape[2]
     dq = torch.empty_like(q)
@@ -158,6 +216,7 @@ def bwd_workspace(q: torch.Tensor) -> torch.Tensor:
 
 def attn_bwd_delta(out, dout, lse, ws) -> None:
     """Phase 1 of the backward: -rowsum(dO * O) and lse * log2(e) into ``ws``."""
+    same_dtype("output and its gradient", out, dout)
     b, t, hq, d = out.shape
     _lib.check(_lib.LIB.mf_attn_bwd_delta(_ptr(out), _ptr(dout), _ptr(lse), dtype_code(out), b, t,
                                           hq, d, _ptr(ws), ws.numel(), _stream(out.device)))
@@ -165,6 +224,8 @@ def attn_bwd_delta(out, dout, lse, ws) -> None:
 
 def attn_bwd_dq(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, dq) -> None:
     """Phase 2 of the backward: dq (reads the delta phase's ``ws``)."""
+    check_attention_operands(q, k, v, plan, mode)
+    same_dtype("query, output gradient and dq", q, dout, dq)
     b, t, hq, d = q.shape
     s, hkv = k.shape[1], k.shape[2]
     _lib.check(_lib.LIB.mf_attn_bwd_dq(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse),
@@ -175,6 +236,8 @@ def attn_bwd_dq(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, dq)
 
 def attn_bwd_dkdv(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, dk, dv) -> None:
     """Phase 3 of the backward: dk and dv (reads the delta phase's ``ws``)."""
+    check_attention_operands(q, k, v, plan, mode)
+    same_dtype("query, output gradient, dk and dv", q, dout, dk, dv)
     b, t, hq, d = q.shape
     s, hkv = k.shape[1], k.shape[2]
     _lib.check(_lib.LIB.mf_attn_bwd_dkdv(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse),
@@ -183,14 +246,34 @@ def attn_bwd_dkdv(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, d
                                          ws.numel(), _stream(q.device)))
 
 
+def _check_decode_shapes(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    if (q.dim() != 4 or q.shape[1] != 1 or k_cache.dim() != 4 or k_cache.shape != v_cache.shape
+            or k_cache.shape[0] != q.shape[0] or k_cache.shape[3] != q.shape[3]):
+        raise ValueError("Cached attention query/KV shapes are incompatible")
+
+
+def _check_lengths(lengths: torch.Tensor, batch: int, what: str) -> None:
+    if lengths.dtype != torch.int32 or tuple(lengths.shape) != (batch,) \
+            or not lengths.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous int32 [{batch}] tensor")
+
+
 def decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                   k_cache: torch.Tensor, v_cache: torch.Tensor, positions: torch.Tensor,
                   scale: float) -> torch.Tensor:
     """Write each row's new key/value into its cache slot (in place), then decode."""
-    device = require_device(q, k_new, v_new, k_cache, v_cache, positions)
-    code = dtype_code(q)
+    code = same_dtype("query, new key/value and the KV caches", q, k_new, v_new, k_cache, v_cache)
+    _check_decode_shapes(q, k_cache, v_cache)
     b, _, hq, d = q.shape
     cap, hkv = k_cache.shape[1], k_cache.shape[2]
+    for t in (k_new, v_new):
+        _require_shape(t, (b, 1, hkv, d), "the new key/value rows")
+    _check_lengths(positions, b, "positions")
+    for t in (k_cache, v_cache):
+        if not t.is_contiguous():
+            raise ValueError("the KV caches must be contiguous to be updated in place")
+    device = require_device(q, k_new, v_new, k_cache, v_cache, positions)
+    q, k_new, v_new = q.contiguous(), k_new.contiguous(), v_new.contiguous()
     out = torch.empty_like(q)
     ws_bytes = _lib.LIB.mf_decode_workspace_bytes(b, cap, hq, d)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
@@ -203,10 +286,13 @@ def decode_append(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
 
 def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
            lengths: torch.Tensor, scale: float) -> torch.Tensor:
-    device = require_device(q, k_cache, v_cache, lengths)
-    code = dtype_code(q)
+    code = same_dtype("query and the KV caches", q, k_cache, v_cache)
+    _check_decode_shapes(q, k_cache, v_cache)
     b, _, hq, d = q.shape
     cap, hkv = k_cache.shape[1], k_cache.shape[2]
+    _check_lengths(lengths, b, "lengths")
+    device = require_device(q, k_cache, v_cache, lengths)
+    q, k_cache, v_cache = q.contiguous(), k_cache.contiguous(), v_cache.contiguous()
     out = torch.empty_like(q)
     ws_bytes = _lib.LIB.mf_decode_workspace_bytes(b, cap, hq, d)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
@@ -216,17 +302,75 @@ def decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     return out
 
 
+class PlanCache:
+    """Plans keyed on the identity and in-place version of the id and mask tensors.
+
+    A plan depends only on ``(segment_ids, mask, mode, lengths)``.  The
+    encoder passes one ``(segment_ids, mask)`` pair to every attention layer
+    (``models/lfm2_5/encoder.py:64-110``) and rematerialisation runs each
+    forward twice, so the block map runs once per distinct pair.  An entry
+    holds weak references to the tensors it was built from: it is used only
+    while both are the very objects passed and their version counters (bumped
+    by every in-place torch write) are unchanged, so a freed, replaced or
+    modified tensor misses.  Writes that bypass torch (a raw pointer handed to
+    other code) are not seen: such callers pass ``plan=`` explicitly or clear
+    the cache.
+    """
+
+    def __init__(self, capacity: int = 8):
+        self.capacity = capacity
+        self.enabled = True
+        self._entries: collections.OrderedDict = collections.OrderedDict()
+        self._lock = threading.Lock()
+
+    @staticmethod
+    def _state(t: torch.Tensor | None):
+        return (None, None) if t is None else (weakref.ref(t), t._version)
+
+    def get(self, segment_ids: torch.Tensor | None, mask: torch.Tensor, mode: int, q_len: int,
+            kv_len: int, batch: int) -> Plan:
+        if not self.enabled:
+            return block_map(segment_ids, mask, mode, q_len, kv_len, batch)
+        key = (id(segment_ids), id(mask), mode, q_len, kv_len, batch, mask.device)
+        with self._lock:
+            entry = self._entries.get(key)
+            if entry is not None:
+                (seg_ref, seg_ver), (mask_ref, mask_ver), plan = entry
+                seg_ok = segment_ids is None if seg_ref is None else (
+                    seg_ref() is segment_ids and segment_ids._version == seg_ver)
+                if seg_ok and mask_ref() is mask and mask._version == mask_ver:
+                    self._entries.move_to_end(key)
+                    return plan
+        plan = block_map(segment_ids, mask, mode, q_len, kv_len, batch)
+        with self._lock:
+            self._entries[key] = (self._state(segment_ids), self._state(mask), plan)
+            while len(self._entries) > self.capacity:
+                self._entries.popitem(last=False)
+        return plan
+
+    def clear(self) -> None:
+        with self._lock:
+            self._entries.clear()
+
+
+PLANS = PlanCache()
+
+
 class PackedAttention(torch.autograd.Function):
     """Masked attention with a HIP forward and a HIP backward.
 
-    ``forward(q, k, v, mask, segment_ids, mode, scale)``: integer inputs get
-    no gradient (the reference's float0 cotangents).
+    ``forward(q, k, v, mask, segment_ids, mode, scale, plan)``: integer inputs
+    get no gradient (the reference's float0 cotangents).  ``plan`` is a
+    :class:`Plan` built for the same ids, mask and mode, or ``None`` to take
+    one from :data:`PLANS`.
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, mask, segment_ids, mode, scale):
+    def forward(ctx, q, k, v, mask, segment_ids, mode, scale, plan=None):
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        plan = block_map(segment_ids, mask, mode, q.shape[1], k.shape[1])
+        check_attention_operands(q, k, v)
+        if plan is None:
+            plan = PLANS.get(segment_ids, mask, mode, q.shape[1], k.shape[1], q.shape[0])
         out, lse = attn_fwd(q, k, v, plan, mode, scale)
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.plan, ctx.mode, ctx.scale = plan, mode, scale
@@ -236,8 +380,9 @@ class PackedAttention(torch.autograd.Function):
     def backward(ctx, dout):
         q, k, v, out, lse = ctx.saved_tensors
         dq, dk, dv = attn_bwd(q, k, v, out, dout.contiguous(), lse, ctx.plan, ctx.mode, ctx.scale)
-        return dq, dk, dv, None, None, None, None
+        return dq, dk, dv, None, None, None, None, None
 
 
-def packed_attention(q, k, v, mask, segment_ids, mode: int, scale: float) -> torch.Tensor:
-    return PackedAttention.apply(q, k, v, mask, segment_ids, mode, scale)
+def packed_attention(q, k, v, mask, segment_ids, mode: int, scale: float,
+                     plan: Plan | None = None) -> torch.Tensor:
+    return PackedAttention.apply(q, k, v, mask, segment_ids, mode, scale, plan)

@@ -28,9 +28,12 @@ of the forward (method of ``tests/layers/test_blocks.py:156-174``), the
 packed-equals-independent-rows invariant (``tests/layers/test_blocks.py:342-382``),
 segment-id permutation invariance, a single-segment case equal to a textbook
 ``scipy.special.softmax`` attention, and the grouped (per-segment) evaluation
-agreeing with the dense grid.  The two bf16 emulations are "parity unpinned" at
-bit level (only a JAX import could pin them); they are used with the 2e-2
-tolerance, and checked to stay within it of the FP64 result.
+agreeing with the dense grid.  The two bf16 emulations are pinned by closed
+forms that move when a cast point moves: rounded probabilities (zero q/k over
+six keys: ``bf16(1/6) * 100`` rounds to 16.75 where ``100/6`` rounds to 16.625),
+the einsum's bf16 logits against SDPA's fp32 logits (raw logits 100 and 100.25
+give P1 = 0.5 against 0.5078125), the rounded output, single-key rows and the
+two agreeing bit for bit when every logit is representable in bf16.
 """
 
 from __future__ import annotations

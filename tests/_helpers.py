@@ -71,3 +71,49 @@ def torch_reference(mode, q, k, v, mask, seg, do):
 
 def max_abs(a: torch.Tensor, b: torch.Tensor) -> float:
     return (a.float() - b.float()).abs().max().item() if a.numel() else 0.0
+
+
+BF16_TOL = 2e-2
+BF16_HALF_ULP = 2.0 ** -8  # bound on |bf16(x) - x| / |x| (8 significant bits, round to nearest)
+
+
+def bf16_errors(a, r) -> tuple[float, float]:
+    """``(max|a - r|, max(|a - r| - 2**-8 |r|))`` element-wise.
+
+    The second figure is the error beyond the one rounding a bf16 result of
+    the exact value ``r`` must carry (|bf16(x) - x| <= 2**-8 |x|): entries of
+    magnitude 10 cannot be held within 2e-2 of their true values in bf16,
+    while the excess stays a plain absolute error for every entry.
+    """
+    a = torch.as_tensor(a).double().cpu()
+    r = torch.as_tensor(r).double().cpu()
+    if not a.numel():
+        return 0.0, 0.0
+    diff = (a - r).abs()
+    return diff.max().item(), (diff - BF16_HALF_ULP * r.abs()).max().item()
+
+
+def check_bf16(label: str, a, r, tol: float = BF16_TOL) -> tuple[float, float]:
+    """Assert the bf16 bar ``max(|a - r| - 2**-8 |r|) < tol`` and log both figures."""
+    raw, excess = bf16_errors(a, r)
+    say(f"{label}: max-abs {raw:.3e} beyond-rounding {excess:.3e}")
+    assert excess < tol, (label, raw, excess)
+    return raw, excess
+
+
+def check_bf16_sum(label: str, a, r, abs_sum, tol: float = BF16_TOL) -> float:
+    """The bf16 bar for a reduction over many rounded terms (a gain or tap gradient).
+
+    Each term carries at most one bf16 rounding of an operand (relative
+    2**-8), so the sum may differ from the exact one by up to 2**-8 times the
+    sum of the terms' magnitudes ``abs_sum``; the bar is the error beyond that:
+    ``max(|a - r| - 2**-8 abs_sum) < tol``.
+    """
+    a = torch.as_tensor(a).double().cpu()
+    r = torch.as_tensor(r).double().cpu()
+    s = torch.as_tensor(abs_sum).double().cpu()
+    diff = (a - r).abs()
+    excess = (diff - BF16_HALF_ULP * s).max().item()
+    say(f"{label}: max-abs {diff.max().item():.3e} beyond-rounding {excess:.3e}")
+    assert excess < tol, (label, diff.max().item(), excess)
+    return excess

@@ -1,9 +1,11 @@
 """GPU parity of the packed attention forward and backward.
 
 Bars: fp32 within 1e-5 (relative, with a 1e-5 floor) of
-the FP64 oracle; bf16 outputs and gradients within max-abs 2e-2 of an fp32
-evaluation of the same bf16 inputs, and within 2e-2 of the reference's bf16
-cast-point emulation where that fits on the CPU.
+the FP64 oracle; bf16 outputs and gradients within 2e-2 of an exact (FP64, or
+fp32 at the full shapes) evaluation of the same bf16 inputs, element-wise and
+beyond the one bf16 rounding of the result (``max(|a - r| - 2**-8 |r|) <
+2e-2``), and within 2e-2 of the reference's bf16 cast-point emulation where
+that fits on the CPU.
 """
 
 import json
@@ -13,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import DT, max_abs, operands, say, torch_reference
+from _helpers import BF16_TOL, DT, check_bf16, max_abs, operands, say, torch_reference
 from mfattn import _lib, ops
 from mfattn.kernels import attention, bidirectional
 from oracle import attention as oatt
@@ -22,23 +24,6 @@ from oracle import masks, packing
 GOLD = pathlib.Path(__file__).parent / "golden"
 FIX = json.loads((GOLD / "reference_fixtures.json").read_text())
 pytestmark = pytest.mark.gpu
-
-BF16_TOL = 2e-2
-
-
-def bf16_scaled_error(a: torch.Tensor, r: torch.Tensor) -> float:
-    """max|a - r| / max(1, max|r|): the 2e-2 max-abs bar at unit scale.
-
-    A bf16 tensor whose entries reach |r| > 5 cannot hold its true values
-    within 2e-2 (its half-ulp there is 2**-8 relative), and the unscaled
-    C3/C5 inputs give gradients with |r| ~ 10; the bar is applied to the
-    tensor's magnitude, i.e. it is plain max-abs 2e-2 for every tensor whose
-    largest entry is at most 1 (the C2 headline workload)."""
-    a, r = a.float(), r.float()
-    if not a.numel():
-        return 0.0
-    return (a - r).abs().max().item() / max(1.0, r.abs().max().item())
-
 
 def _grads(fn, q, k, v, do):
     q, k, v = (x.detach().clone().requires_grad_(True) for x in (q, k, v))
@@ -156,7 +141,7 @@ def test_random_layouts_against_oracle(mode, dtype, t, device):
         if dtype == "float32":
             np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
         else:
-            assert bf16_scaled_error(a.cpu(), torch.tensor(r)) < BF16_TOL, name
+            check_bf16(f"random layout mode {mode} T {t} {name}", a, r)
 
 
 @pytest.mark.parametrize("hq, hkv", [(4, 4), (8, 2), (6, 2), (3, 1), (16, 2), (2, 2)])
@@ -182,7 +167,7 @@ def test_gqa_ratios(hq, hkv, dtype, mode, device):
         if dtype == "float32":
             np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
         else:
-            assert bf16_scaled_error(a.cpu(), torch.tensor(r)) < BF16_TOL, name
+            check_bf16(f"gqa {hq}/{hkv} mode {mode} {name}", a, r)
 
 
 @pytest.mark.parametrize("name", ["C2", "C3", "C5"])
@@ -203,12 +188,9 @@ def test_baseline_config_bf16_fwd_bwd(name, device):
     got = _grads(fn, q, k, v, do)
     ref = torch_reference(mode, q, k, v, w.attention_mask, w.segment_ids, do)
     names = ("out", "dq", "dk", "dv")
-    errs = {n: max_abs(a, r) for n, a, r in zip(names, got, ref)}
-    excess = {n: bf16_scaled_error(a, r) for n, a, r in zip(names, got, ref)}
-    say(name, "max-abs", errs, "scaled", excess,
-        "ref max |x|", {n: r.abs().max().item() for n, r in zip(names, ref)})
-    for n, e in excess.items():
-        assert e < BF16_TOL, (n, e)
+    say(name, "ref max |x|", {n: round(r.abs().max().item(), 3) for n, r in zip(names, ref)})
+    for n, a, r in zip(names, got, ref):
+        check_bf16(f"{name} {n}", a, r)
 
 
 def test_bf16_against_reference_cast_points(device):
@@ -332,4 +314,4 @@ def test_phase_entry_points_match_the_fused_backward(dtype, device):
         if dtype == torch.float32:
             torch.testing.assert_close(a, r, rtol=1e-5, atol=1e-5)
         else:
-            assert bf16_scaled_error(a, r) < BF16_TOL
+            check_bf16("phase entry points vs fused", a, r)

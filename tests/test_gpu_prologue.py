@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import say
+from _helpers import check_bf16, check_bf16_sum, say
 from mfattn.kernels import prologue
 from oracle import packing
 from oracle import prologue as oprol
@@ -13,14 +13,12 @@ from oracle import prologue as oprol
 pytestmark = pytest.mark.gpu
 
 
-def _scaled_error(a, r):
-    a, r = np.asarray(a, np.float64), np.asarray(r, np.float64)
-    return np.abs(a - r).max() / max(1.0, np.abs(r).max())
-
-
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("theta", [10000.0, 1000000.0])
 def test_qk_norm_rope_matches_the_oracle(dtype, theta, device):
+    """fp32 against the FP64 prologue; bf16 against the reference's cast order (every
+    operation rounded to bf16), which already carries five roundings an FP64 evaluation
+    does not have."""
     rng = np.random.default_rng(20)
     w = packing.make_workload("C1")
     b, t, hq, hkv, d = w.batch, w.length, 16, 8, 64
@@ -32,14 +30,104 @@ def test_qk_norm_rope_matches_the_oracle(dtype, theta, device):
     tq, tk = (torch.tensor(x, device=device).to(dtype) for x in (q, k))
     gq, gk = prologue.qk_norm_rope(tq, tk, torch.tensor(qg), torch.tensor(kg),
                                    torch.tensor(pos), eps=1e-5, rope_theta=theta)
+    if dtype == torch.float32:
+        rq, rk = oprol.qk_norm_rope(q, k, qg, kg, pos, 1e-5, theta)
+        for name, got, ref in (("q", gq, rq), ("k", gk, rk)):
+            np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-5, atol=1e-5, err_msg=name)
+    else:
+        # the reference's cast order (torch-CPU bf16): bit for bit almost everywhere; where
+        # the kernel's fp32 cos/sin or rsqrt differ from torch's in the last bit, a rounded
+        # cos, sin or normalised value moves by one bf16 ulp, which moves a rotation
+        # product by at most 2**-7 of its operand's magnitude (and, after cancellation in
+        # the sum, possibly several ulps of the result): the bar is two such steps
+        eq = oprol.qk_norm_rope_cast(torch.tensor(q).to(dtype), torch.tensor(k).to(dtype),
+                                     torch.tensor(qg), torch.tensor(kg), pos, 1e-5, theta)
+        for name, got, ref, x, gain in (("q", gq, eq[0], q, qg), ("k", gk, eq[1], k, kg)):
+            got = got.cpu()
+            n = oprol.rms_norm_cast(torch.tensor(x).to(dtype), torch.tensor(gain), 1e-5).float()
+            bound = 2.0 ** -6 * (n.abs() + torch.cat((n[..., 32:], n[..., :32]), -1).abs())
+            diff = (got.float() - ref.float()).abs()
+            exact = (got == ref).float().mean().item()
+            say(f"prologue {name} vs cast order: exact {exact:.6f}, max diff {diff.max().item():.3e},"
+                f" max diff / bound {(diff / bound.clamp_min(1e-30)).max().item():.3f}")
+            assert bool((diff <= bound).all()), name
+            assert exact > 0.999, name
+
+
+def test_hand_derived_bf16_cases_on_the_device(device):
+    """The cast-order cases of tests/test_oracle_prologue.py, through the kernel."""
+    from test_oracle_prologue import PROLOGUE_CASES
+
+    say("prologue hand cases")
+    for x0, x32, x5, g0, g32, p, want, _ in PROLOGUE_CASES:
+        x = torch.zeros(1, 1, 1, 64)
+        x[0, 0, 0, 0], x[0, 0, 0, 32], x[0, 0, 0, 5] = x0, x32, x5
+        gain = torch.ones(64)
+        gain[0], gain[32] = g0, g32
+        xb = x.to(device, torch.bfloat16)
+        out, _ = prologue.qk_norm_rope(xb, xb.clone(), gain, gain, torch.tensor([[p]]), eps=1e-6,
+                                       rope_theta=10000.0)
+        assert (out[0, 0, 0, 0].item(), out[0, 0, 0, 32].item()) == want
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_qk_norm_rope_backward_matches_the_fp64_vjp(dtype, device):
+    """mf_qk_norm_rope_bwd through autograd against the analytic FP64 VJP (itself pinned
+    by central differences): dq, dk element-wise; the gain gradients, sums over every
+    token and head, with the reduction bar."""
+    rng = np.random.default_rng(23)
+    w = packing.make_workload("C1")
+    b, t, hq, hkv, d = w.batch, w.length, 16, 8, 64
+    say("prologue backward", dtype)
+    pos = oprol.segment_positions(w.segment_ids)
+    q = (rng.standard_normal((b, t, hq, d)) * 2).astype(np.float32)
+    k = rng.standard_normal((b, t, hkv, d)).astype(np.float32)
+    qg, kg = (1 + 0.1 * rng.standard_normal((2, d))).astype(np.float32)
+    gq, gk = rng.standard_normal((b, t, hq, d)).astype(np.float32), \
+        rng.standard_normal((b, t, hkv, d)).astype(np.float32)
+    dev = lambda x: torch.tensor(x, device=device).to(dtype).requires_grad_(True)  # noqa: E731
+    tq, tk = dev(q), dev(k)
+    tqg = torch.tensor(qg, device=device, requires_grad=True)
+    tkg = torch.tensor(kg, device=device, requires_grad=True)
+    oq, ok = prologue.qk_norm_rope(tq, tk, tqg, tkg, torch.tensor(pos), eps=1e-5, rope_theta=1e4)
+    assert oq.grad_fn is not None and ok.grad_fn is not None
+    torch.autograd.backward((oq, ok), (torch.tensor(gq, device=device).to(dtype),
+                                       torch.tensor(gk, device=device).to(dtype)))
     cast = lambda x: torch.tensor(x).to(dtype).double().numpy()  # noqa: E731
-    rq, rk = oprol.qk_norm_rope(cast(q), cast(k), cast(qg), cast(kg), pos, 1e-5, theta)
-    for name, got, ref in (("q", gq, rq), ("k", gk, rk)):
-        got = got.double().cpu().numpy()
-        if dtype == torch.float32:
-            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5, err_msg=name)
-        else:
-            assert _scaled_error(got, ref) < 2e-2, name
+    rdq, rdk, rdqg, rdkg, aq, ak = oprol.qk_norm_rope_vjp(
+        cast(q), cast(k), cast(qg), cast(kg), pos, 1e-5, 1e4, cast(gq), cast(gk), with_abs=True)
+    got = (tq.grad, tk.grad, tqg.grad, tkg.grad)
+    if dtype == torch.float32:
+        for name, a, r in zip(("dq", "dk", "dq_gain", "dk_gain"), got, (rdq, rdk, rdqg, rdkg)):
+            scale = max(1.0, float(np.abs(r).max()))
+            np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5 * scale,
+                                       err_msg=name)
+    else:
+        check_bf16("prologue bwd dq", got[0], rdq)
+        check_bf16("prologue bwd dk", got[1], rdk)
+        check_bf16_sum("prologue bwd dq_gain", got[2], rdqg, aq)
+        check_bf16_sum("prologue bwd dk_gain", got[3], rdkg, ak)
+
+
+def test_backward_is_deterministic_and_in_place_refuses_gradients(device):
+    rng = np.random.default_rng(24)
+    say("prologue backward determinism")
+    b, t = 2, 300
+    q = torch.tensor(rng.standard_normal((b, t, 4, 64)), dtype=torch.bfloat16, device=device)
+    k = torch.tensor(rng.standard_normal((b, t, 2, 64)), dtype=torch.bfloat16, device=device)
+    g = torch.ones(64, device=device)
+    runs = []
+    for _ in range(2):
+        tq, tk = q.clone().requires_grad_(True), k.clone().requires_grad_(True)
+        tg = g.clone().requires_grad_(True)
+        oq, ok = prologue.qk_norm_rope(tq, tk, tg, tg, None, eps=1e-6, rope_theta=500.0)
+        (oq.float().sum() + 2 * ok.float().sum()).backward()
+        runs.append((tq.grad, tk.grad, tg.grad))
+    for x, y in zip(*runs):
+        assert torch.equal(x, y)
+    with pytest.raises(ValueError, match="inplace"):
+        prologue.qk_norm_rope(q.clone().requires_grad_(True), k, g, g, None, eps=1e-6,
+                              rope_theta=500.0, inplace=True)
 
 
 def test_positions_forms_and_in_place(device):

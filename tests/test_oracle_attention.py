@@ -179,3 +179,67 @@ def test_bf16_emulations_stay_within_tolerance_of_fp64():
         out = fn(tq, tk, tv, torch.tensor(valid[:, None]))
         out = torch.where(torch.tensor(present[:, :, None, None]), out.float(), 0.0).numpy()
         assert np.abs(out - ref).max() < 2e-2
+
+
+# bf16 cast points of the two emulations, pinned by closed forms that move when a cast
+# point moves (one head, D = 64, scale 1/8; bf16 keeps 8 significant bits).
+
+
+def _bf(x):
+    return torch.tensor(np.asarray(x, np.float32)).to(torch.bfloat16)
+
+
+def test_bf16_emulations_round_the_probabilities_and_the_output():
+    """Zero q/k over 6 keys: P = bf16(1/6) = 0.1669921875 exactly.  With V = [100, 0, ...]
+    the output is bf16(100 * 0.1669921875) = bf16(16.699...) = 16.75; unrounded
+    probabilities would give bf16(16.666...) = 16.625."""
+    q, k = _bf(np.zeros((1, 1, 1, 64))), _bf(np.zeros((1, 6, 1, 64)))
+    v = np.zeros((1, 6, 1, 64), np.float32)
+    v[0, 0, 0, 0] = 100.0
+    valid = torch.ones(1, 1, 1, 6, dtype=torch.bool)
+    for fn in (oatt.dense_bf16_einsum, oatt.sdpa_bf16):
+        out = fn(q, k, _bf(v), valid)
+        assert out.dtype == torch.bfloat16
+        assert out[0, 0, 0, 0].item() == 16.75, fn.__name__
+        assert out[0, 0, 0, 1].item() == 0.0
+
+
+def test_einsum_emulation_rounds_the_logits_and_sdpa_does_not():
+    """q = (1, 1, 0, ...), keys (100, 0, ...) and (100, 0.25, ...): raw logits 100 and 100.25.
+    attention.py:23-25 makes the einsum result bf16, and bf16(100.25) = 100 (a tie, to
+    even), so both scaled logits are 12.5 and P = (0.5, 0.5).  SDPA keeps fp32 logits 12.5
+    and 12.53125: P1 = 1 / (1 + e^-0.03125) = 0.5078119..., bf16 0.5078125, and
+    P0 = 0.4921881..., bf16 0.4921875.  V = (0, 1) in dimension 0 reads P1 off."""
+    q = np.zeros((1, 1, 1, 64), np.float32)
+    q[..., :2] = 1.0
+    k = np.zeros((1, 2, 1, 64), np.float32)
+    k[0, :, 0, 0] = 100.0
+    k[0, 1, 0, 1] = 0.25
+    v = np.zeros((1, 2, 1, 64), np.float32)
+    v[0, 1, 0, 0] = 1.0
+    valid = torch.ones(1, 1, 1, 2, dtype=torch.bool)
+    dense = oatt.dense_bf16_einsum(_bf(q), _bf(k), _bf(v), valid)
+    sdpa = oatt.sdpa_bf16(_bf(q), _bf(k), _bf(v), valid)
+    assert dense[0, 0, 0, 0].item() == 0.5
+    assert sdpa[0, 0, 0, 0].item() == 0.5078125
+
+
+def test_bf16_emulations_on_single_keys_and_representable_logits():
+    """A row with one valid key returns that key's value exactly (P = 1); with integer q/k
+    every logit is exactly representable in bf16, so the two emulations agree bit for bit
+    (they differ only in the logits' cast and the masked fill, which a row with a valid key
+    never sees)."""
+    rng = np.random.default_rng(5)
+    q = rng.integers(-2, 3, size=(2, 9, 4, 64)).astype(np.float32)
+    k = rng.integers(-2, 3, size=(2, 9, 2, 64)).astype(np.float32)
+    v = rng.standard_normal((2, 9, 2, 64)).astype(np.float32)
+    seg = np.array([[1, 1, 2, 2, 2, 3, 4, 4, 0], [5, 5, 5, 5, 5, 5, 5, 5, 6]])
+    valid, present = masks.bidirectional_valid(seg != 0, seg)
+    tv = torch.tensor(valid[:, None])
+    dense = oatt.dense_bf16_einsum(_bf(q), _bf(k), _bf(v), tv)
+    sdpa = oatt.sdpa_bf16(_bf(q), _bf(k), _bf(v), tv)
+    assert torch.equal(dense[torch.tensor(present)], sdpa[torch.tensor(present)])
+    vb = _bf(v)
+    for row, t in ((0, 5), (1, 8)):  # single-token segments 3 and 6
+        torch.testing.assert_close(dense[row, t], vb[row, t].repeat_interleave(2, dim=0),
+                                   rtol=0, atol=0)
