@@ -59,6 +59,8 @@ EXPORTS = (
     "mf_segmented_conv",
     "mf_segmented_conv_bwd_workspace_bytes",
     "mf_segmented_conv_bwd",
+    "mf_static_scratch_bytes",
+    "mf_decode_static",
     "mf_last_error",
     "mf_version",
 )
@@ -135,6 +137,10 @@ def _load() -> ctypes.CDLL:
     lib.mf_block_map_placements.restype = i32
     lib.mf_segmented_conv.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, vp, vp]
     lib.mf_segmented_conv.restype = i32
+    lib.mf_static_scratch_bytes.argtypes = []
+    lib.mf_static_scratch_bytes.restype = sz
+    lib.mf_decode_static.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, f32, vp, vp]
+    lib.mf_decode_static.restype = i32
     lib.mf_last_error.argtypes = []
     lib.mf_last_error.restype = ctypes.c_char_p
     lib.mf_version.argtypes = []
