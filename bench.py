@@ -25,9 +25,13 @@
   probabilities; fwd + autograd bwd), timed per (row, KV-group) chunk of the
   same C2 batch for about ``--cpu-seconds`` and scaled to useful TFLOP/s.
 
-``--config C3`` or ``--config C5`` times the same step on the causal packed
-workloads instead (C3: 4 x 8192, mean segment 512; C5: 1 x 32768, segments of
-16-128 tokens) and prints the step's line alone.
+* ``configs`` = the same step on the causal packed workloads C3 (4 x 8192,
+  mean segment 512) and C5 (1 x 32768, segments of 16-128 tokens): ms per
+  step, useful TFLOP/s and the fraction of the max(MFMA, HBM) roofline time.
+
+The decode, the rows and C3/C5 are measured before the C2 step, so the GPU's
+clocks are at their steady state when the headline is timed.
+``--config C3`` or ``--config C5`` prints one of those step lines alone.
 
 Only one GPU is used; ``--gpus`` above 1 exits with a message.
 """
@@ -79,7 +83,6 @@ def _traffic(kernel: str, workload: str):
 
 
 def gpu_leg(steps: int, warmup: int, profile: bool = False, name: str = "C2", decode: bool = True):
-    import numpy as np
     import torch
 
     from mfattn import _lib, ops, workloads
@@ -87,10 +90,12 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False, name: str = "C2", de
     dev = torch.device("cuda:0")
     w = workloads.packed(name)
     mode = _lib.MODE_PACKED_CAUSAL if w.causal else _lib.MODE_PACKED_BIDIR
-    rng = np.random.default_rng(w.seed)
+    # operands drawn on the device (seeded): no host-side pause between the
+    # previous measurement and this one's warm-up, so the clocks stay up
+    gen = torch.Generator(device=dev).manual_seed(w.seed)
 
     def mk(shape, scale):
-        return torch.tensor(rng.standard_normal(shape).astype(np.float32) * scale, device=dev).to(torch.bfloat16)
+        return (torch.randn(shape, generator=gen, device=dev) * scale).to(torch.bfloat16)
 
     q = mk((w.batch, w.length, w.q_heads, w.head_dim), w.qkv_scale)
     k = mk((w.batch, w.length, w.kv_heads, w.head_dim), w.qkv_scale)
@@ -154,6 +159,7 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False, name: str = "C2", de
             for i, name in enumerate(names)}
     kern["attn_bwd_dq"] = kern["attn_bwd"] - kern["attn_bwd_dkdv"]
     flops = workloads.attention_flops(w)
+    nbytes = workloads.attention_bytes(w)["fwd_bwd"]
     algo = {"attn_fwd": flops["fwd"], "attn_bwd_dq": flops["dq"], "attn_bwd_dkdv": flops["dkdv"]}
     dominant = max(algo, key=lambda name: kern[name])
     achieved = algo[dominant] / (kern[dominant] * 1e-3) / 1e12
@@ -173,6 +179,15 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False, name: str = "C2", de
                      "algorithmic_gflop_per_launch": algo[dominant] / 1e9},
         "fa2_convention_tflops": flops["fwd_bwd_fa2"] / (ms * 1e-3) / 1e12,
         "step_roofline_frac": (flops["fwd_bwd"] / (MFMA_BF16_PEAK_TFLOPS * 1e12)) / (ms * 1e-3),
+        # the step against max(MFMA, HBM) roofline time (BASELINE.md accounting)
+        "step_roofline": {
+            "mfma_us": flops["fwd_bwd"] / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e6,
+            "hbm_us": nbytes / (HBM_PEAK_GBPS * 1e9) * 1e6,
+            "bound": "mfma" if flops["fwd_bwd"] / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+            >= nbytes / (HBM_PEAK_GBPS * 1e9) else "hbm",
+            "frac": max(flops["fwd_bwd"] / (MFMA_BF16_PEAK_TFLOPS * 1e12),
+                        nbytes / (HBM_PEAK_GBPS * 1e9)) / (ms * 1e-3),
+            "algorithmic_bytes": nbytes},
         "kernels_ms": kern,
     }
     del q, k, v, do, dq, dk, dv, out, lse, plan, ws
@@ -506,9 +521,23 @@ def main() -> int:
                           "ms_per_step": gpu["ms_per_step"], "higher_is_better": True,
                           "dtype": "bf16", "config": gpu["config"], "roofline": gpu["roofline"],
                           "kernels_ms": gpu["kernels_ms"],
-                          "step_roofline_frac": gpu["step_roofline_frac"]}))
+                          "step_roofline_frac": gpu["step_roofline_frac"],
+                          "step_roofline": gpu["step_roofline"]}))
         return 0
-    gpu = gpu_leg(args.steps, args.warmup)
+    # The other measurements run first: their GPU work also brings the clocks to
+    # their steady state before the headline C2 step is timed.
+    decode = decode_leg(args.steps, args.warmup)
+    rows = rows_leg(args.steps)
+    configs = {}
+    for name in ("C3", "C5"):
+        other = gpu_leg(args.steps, args.warmup, name=name, decode=False)
+        configs[name] = {"workload": other["config"]["workload"],
+                         "ms_per_step": other["ms_per_step"],
+                         "useful_tflops": other["value"],
+                         "useful_gflop_per_step": other["config"]["useful_gflop_per_step"],
+                         "step_roofline": other["step_roofline"],
+                         "kernels_ms": other["kernels_ms"]}
+    gpu = gpu_leg(args.steps, args.warmup, decode=False)
     line = {
         "metric": METRIC,
         "value": gpu["value"],
@@ -525,11 +554,13 @@ def main() -> int:
         "config": gpu["config"],
         "roofline": gpu["roofline"],
         "cpu_baseline": None if args.no_cpu_baseline else cpu_leg(args.cpu_seconds),
-        "decode": gpu["decode"],
+        "decode": decode,
+        "configs": configs,
         "kernels_ms": gpu["kernels_ms"],
-        "rows": rows_leg(args.steps),
+        "rows": rows,
         "fa2_convention_tflops": gpu["fa2_convention_tflops"],
         "step_roofline_frac": gpu["step_roofline_frac"],
+        "step_roofline": gpu["step_roofline"],
         "wall_ms_per_step": gpu["wall_ms_per_step"],
     }
     print(json.dumps(line))
