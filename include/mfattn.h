@@ -255,11 +255,10 @@ int mf_segmented_conv_bwd(const void* b_gate, const void* c_gate,
  * hipMalloc); no counterpart in the reference.  The same kernels as mf_decode
  * run on a static device array of MF_STATIC_SCRATCH_BYTES that every GPU the
  * library runs on holds until the process ends; calls whose decode workspace
- * (mf_decode_workspace_bytes for bf16 sizes it at the fp32 chunk; the
- * static call needs the dtype's own) exceeds it return MF_ERR_WORKSPACE
- * before anything is enqueued.  Calls that overlap on one GPU share the
+ * (mf_decode_workspace_bytes) exceeds it return MF_ERR_WORKSPACE before
+ * anything is enqueued.  Calls that overlap on one GPU share the
  * array and race: order them on one stream.  Nothing is allocated. */
-#define MF_STATIC_SCRATCH_BYTES ((size_t)16 << 20)
+#define MF_STATIC_SCRATCH_BYTES ((size_t)32 << 20)
 size_t mf_static_scratch_bytes(void);
 int mf_decode_static(const void* q, const void* k_cache, const void* v_cache,
                      const int32_t* lengths, int dtype, int batch, int capacity,

@@ -21,6 +21,7 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
                            int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
                            void* dk, void* dv, float* workspace, int phases, hipStream_t stream);
 size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk);
+size_t decode_workspace_bytes_any(int batch, int cap, int Hq);
 int decode_chunk(bool f32);
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
                          bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
@@ -267,8 +268,7 @@ int mf_attn_bwd_dkdv(const void* q, const void* k, const void* v, const void* do
 
 size_t mf_decode_workspace_bytes(int batch, int capacity, int q_heads, int head_dim) {
   if (batch < 1 || capacity < 1 || q_heads < 1 || head_dim != mf::kD) return 0;
-  // bf16 uses the smaller chunk count; size for the fp32 chunk (the larger one)
-  return mf::decode_workspace_bytes(batch, capacity, q_heads, mf::decode_chunk(true));
+  return mf::decode_workspace_bytes_any(batch, capacity, q_heads);
 }
 
 namespace {

@@ -533,6 +533,194 @@ __global__ __launch_bounds__(512) void decode_bf16_kernel(DecArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 decode over whole token rows: one wave per (row, 128-token chunk)
+// item covering every KV head.  A token's K (or V) row -- Hkv heads x 128 B,
+// contiguous in the [B, cap, Hkv, 64] cache -- is read by 8 * Hkv lanes with
+// one non-temporal 16-byte load each, so a wave streams the chunk's rows as
+// one contiguous range (the access pattern that reaches the HBM read
+// ceiling on this part, where one wave per (row, chunk, head) reads 8
+// separate 128-byte pieces per instruction).  Lane = (token j of the TPL =
+// 8 / Hkv tokens a load covers, head h, 8-dim slice dl).  Per token the
+// lane's 8 dims of the G query heads of group h are dotted with its K slice
+// (v_dot2) and reduced over the 8 lanes of (j, h) with DPP, so every lane of
+// the group holds the same score; the online softmax state (max, sum) and
+// the P V accumulator of its 8 dims live in the lane.  8 tokens of K and V
+// are in flight per lane (16 loads).  Lanes of different j merge their
+// states at the end (log-sum-exp), and the (max, sum, acc) of the chunk go
+// to the partial buffer the combine kernel reads.
+// ---------------------------------------------------------------------------
+constexpr int kRowChunk = 128;  // tokens per work item of the row kernel
+constexpr int kRowUnroll = 8;   // tokens per lane in flight (K and V)
+
+__device__ __forceinline__ u32x4 ld_nt(const bf16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// merge two online-softmax states (max in log2 units m2, sum l, acc[8])
+template <int G>
+__device__ __forceinline__ void merge_lanes(float (&m2)[G], float (&l)[G], float (&acc)[G][8],
+                                            int xor_mask) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float mo = __shfl_xor(m2[g], xor_mask);
+    const float lo = __shfl_xor(l[g], xor_mask);
+    const float mn = fmaxf(m2[g], mo);
+    // a state with no key yet has max -inf and zero sum/acc: weight 0
+    const float wa = m2[g] == kNegInf ? 0.f : fast_exp2(m2[g] - mn);
+    const float wb = mo == kNegInf ? 0.f : fast_exp2(mo - mn);
+    l[g] = l[g] * wa + lo * wb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float ao = __shfl_xor(acc[g][i], xor_mask);
+      acc[g][i] = acc[g][i] * wa + ao * wb;
+    }
+    m2[g] = mn;
+  }
+}
+
+// Chunk count of rows base + lane for the row kernel (0 past the batch).
+__device__ __forceinline__ int row_chunks_c(const DecArgs& a, int base, int chunk) {
+  const int r = base + (threadIdx.x & 63);
+  return r < a.B ? (eff_len(raw_length(a.lengths, a.positions, r), a.cap) + chunk - 1) / chunk : 0;
+}
+
+template <int G, int TPL>
+__global__ __launch_bounds__(256) void decode_rows_kernel(DecArgs a) {
+  constexpr int kHkv = 8 / TPL;
+  const int lane = threadIdx.x & 63;
+  const int j = lane / (8 * kHkv);           // token of a load
+  const int h = (lane >> 3) % kHkv;          // KV head
+  const int dl = lane & 7;                   // 8-dim slice
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // (row, chunk) of this item: rows' chunk counts scanned 64 rows at a time
+  int b = -1, chunk = 0;
+  for (int base = 0, carry = 0; base < a.B; base += 64) {
+    const int incl = wave_prefix(row_chunks_c(a, base, kRowChunk));
+    const int tot = __shfl(incl, 63);
+    if (item < carry + tot) {
+      const int k = __popcll(__ballot(carry + incl <= item));
+      b = base + k;
+      chunk = item - carry - (k > 0 ? __shfl(incl, k - 1) : 0);
+      break;
+    }
+    carry += tot;
+  }
+  b = uniform(b);
+  if (b < 0) return;  // past the last item (the grid is sized for full rows)
+  chunk = uniform(chunk);
+  const float c = a.scale_log2;
+  const float tau2 = 8.f;  // lazy rescale threshold, log2 units
+  const int raw = uniform(raw_length(a.lengths, a.positions, b));
+  const bool flat = raw <= 0;  // every slot masked: uniform weights
+  const int len = eff_len(raw, a.cap);
+  const int t0 = chunk * kRowChunk;
+  const int last = t0 + min(kRowChunk, len - t0) - 1;
+  const int slot = a.positions ? uniform(min(max(a.positions[b], 0), a.cap - 1)) : -1;
+  const size_t row_elems = (size_t)kHkv * kD;  // one token's row
+  const bf16* kbase = reinterpret_cast<const bf16*>(a.k) + (size_t)b * a.cap * row_elems;
+  const bf16* vbase = reinterpret_cast<const bf16*>(a.v) + (size_t)b * a.cap * row_elems;
+  const size_t lane_off = (size_t)h * kD + 8 * dl;
+  const bf16* knew = reinterpret_cast<const bf16*>(a.k_new) + (size_t)b * row_elems + lane_off;
+  const bf16* vnew = reinterpret_cast<const bf16*>(a.v_new) + (size_t)b * row_elems + lane_off;
+
+  u32x4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qv[g] = ld_u32x4(reinterpret_cast<const bf16*>(a.q) + ((size_t)b * a.Hq + h * G + g) * kD + 8 * dl);
+  float m2[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m2[g] = kNegInf;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+  }
+  // this lane's tokens: t0 + j + TPL * u; loads clamp past the chunk's end
+  // (always in bounds), and the token at the append slot reads the new row
+  constexpr int kStep = TPL * kRowUnroll;  // tokens per iteration over the wave
+  for (int tb = t0; tb <= last; tb += kStep) {
+    u32x4 kr[kRowUnroll], vr[kRowUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int t = min(tb + j + TPL * u, last);
+      if (t == slot) {
+        kr[u] = ld_u32x4(knew);
+        vr[u] = ld_u32x4(vnew);
+      } else {
+        kr[u] = ld_nt(kbase + (size_t)t * row_elems + lane_off);
+        vr[u] = ld_nt(vbase + (size_t)t * row_elems + lane_off);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s[kRowUnroll];
+      float mx = kNegInf;
+#pragma unroll
+      for (int u = 0; u < kRowUnroll; ++u) {
+        float x = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x = dot2_bf16(qv[g][i], kr[u][i], x);
+        x = group8_sum(x) * c;  // log2 units
+        s[u] = tb + j + TPL * u <= last ? (flat ? 0.f : x) : kNegInf;
+        mx = fmaxf(mx, s[u]);
+      }
+      if (mx > m2[g] + tau2) {
+        const float alpha = m2[g] == kNegInf ? 0.f : fast_exp2(m2[g] - mx);
+        m2[g] = mx;
+        l[g] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+      }
+      // a lane that has seen no valid token yet keeps max -inf: shift by 0
+      const float shift = m2[g] == kNegInf ? 0.f : m2[g];
+      float p[kRowUnroll];
+#pragma unroll
+      for (int u = 0; u < kRowUnroll; ++u) {
+        p[u] = fast_exp2(s[u] - shift);
+        l[g] += p[u];
+      }
+      // P V: bf16 pairs over tokens (u, u + 1)
+#pragma unroll
+      for (int up = 0; up < kRowUnroll / 2; ++up) {
+        const bf16x2_t pp = {(bf16)p[2 * up], (bf16)p[2 * up + 1]};
+        const uint32_t pw = __builtin_bit_cast(uint32_t, pp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t va = vr[2 * up][i], vb = vr[2 * up + 1][i];
+          const uint32_t lo16 = __builtin_amdgcn_perm(vb, va, 0x05040100u);
+          const uint32_t hi16 = __builtin_amdgcn_perm(vb, va, 0x07060302u);
+          acc[g][2 * i] = dot2_bf16(pw, lo16, acc[g][2 * i]);
+          acc[g][2 * i + 1] = dot2_bf16(pw, hi16, acc[g][2 * i + 1]);
+        }
+      }
+    }
+  }
+  if (slot >= t0 && slot <= last && j == 0) {
+    // the append: this item's chunk holds the slot; write the new row
+    const size_t dst = ((size_t)b * a.cap + slot) * row_elems + lane_off;
+    st_u32x4(reinterpret_cast<bf16*>(a.k_cache) + dst, ld_u32x4(knew));
+    st_u32x4(reinterpret_cast<bf16*>(a.v_cache) + dst, ld_u32x4(vnew));
+  }
+  // lanes of different tokens j hold partial states of the same heads
+  if constexpr (TPL >= 2) merge_lanes<G>(m2, l, acc, 32);
+  if constexpr (TPL >= 4) merge_lanes<G>(m2, l, acc, 16);
+  if constexpr (TPL >= 8) merge_lanes<G>(m2, l, acc, 8);
+  if (j != 0) return;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float* dst = a.partial + (((size_t)b * a.Hq + h * G + g) * a.maxc + chunk) * (2 + kD);
+    f32x4 lo = {acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+    f32x4 hi = {acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+    *reinterpret_cast<f32x4*>(dst + 2 + 8 * dl) = lo;
+    *reinterpret_cast<f32x4*>(dst + 2 + 8 * dl + 4) = hi;
+    if (dl == 0) {
+      dst[0] = m2[g];
+      dst[1] = l[g];
+    }
+  }
+}
+
 // One block of kCombineWaves waves per (row, query head).  Every wave
 // combines the chunk maxima and sums lane-parallel over chunks (the same
 // values in every wave); wave w then accumulates the weighted partial outputs
@@ -579,7 +767,21 @@ size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk) {
          sizeof(float) * (size_t)batch * Hq * maxc * (2 + kD);
 }
 
+// Tokens per partial of the path a call takes: the row kernel (bf16, G and
+// Hkv in {1, 2, 4, 8}), the older bf16 streaming kernel (other power-of-two
+// G), or the LDS-staged kernels (fp32, other G).
 int decode_chunk(bool f32) { return f32 ? 128 : kDecChunk; }
+
+bool decode_rows_path(bool f32, int G, int Hkv) {
+  return !f32 && (G == 1 || G == 2 || G == 4 || G == 8) &&
+         (Hkv == 1 || Hkv == 2 || Hkv == 4 || Hkv == 8);
+}
+
+// workspace bytes that serve every path (the smallest chunk has the most
+// partials)
+size_t decode_workspace_bytes_any(int batch, int cap, int Hq) {
+  return decode_workspace_bytes(batch, cap, Hq, kRowChunk < 128 ? kRowChunk : 128);
+}
 
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
                          bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
@@ -601,7 +803,8 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
   a.Hq = Hq;
   a.Hkv = Hkv;
   a.G = Hq / Hkv;
-  a.chunk = decode_chunk(f32);
+  const bool rows = decode_rows_path(f32, a.G, Hkv);
+  a.chunk = rows ? kRowChunk : decode_chunk(f32);
   a.maxc = (cap + a.chunk - 1) / a.chunk;
   a.scale_log2 = scale * kLog2e;
   char* ws = reinterpret_cast<char*>(workspace);
@@ -627,6 +830,25 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
     hipLaunchKernelGGL((decode_kernel<true>), dim3(gx, Hkv), dim3(256), 0, stream, a);
     hipLaunchKernelGGL((decode_combine_kernel<true>), dim3(batch * Hq), dim3(64 * kCombineWaves), 0,
                        stream, a);
+    return hipGetLastError();
+  }
+  if (rows) {
+    // one wave per (row, chunk) item; the grid covers full rows, waves past
+    // the last item exit at once
+    const long long waves = (long long)batch * a.maxc;
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    switch (a.G * 16 + Hkv) {
+#define MF_ROWS(GG, HH) \
+  case GG * 16 + HH: hipLaunchKernelGGL((decode_rows_kernel<GG, 8 / HH>), grid, dim3(256), 0, stream, a); break;
+      MF_ROWS(1, 1) MF_ROWS(1, 2) MF_ROWS(1, 4) MF_ROWS(1, 8)
+      MF_ROWS(2, 1) MF_ROWS(2, 2) MF_ROWS(2, 4) MF_ROWS(2, 8)
+      MF_ROWS(4, 1) MF_ROWS(4, 2) MF_ROWS(4, 4) MF_ROWS(4, 8)
+      MF_ROWS(8, 1) MF_ROWS(8, 2) MF_ROWS(8, 4) MF_ROWS(8, 8)
+#undef MF_ROWS
+      default: return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL((decode_combine_kernel<false>), dim3(batch * Hq), dim3(64 * kCombineWaves),
+                       0, stream, a);
     return hipGetLastError();
   }
   // bf16: persistent grid of 4-wave blocks over (chunk item, KV head)

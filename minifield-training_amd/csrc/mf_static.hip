@@ -17,8 +17,7 @@
 #include "mf_common.h"
 
 namespace mf {
-size_t decode_workspace_bytes(int batch, int cap, int Hq, int chunk);
-int decode_chunk(bool f32);
+size_t decode_workspace_bytes_any(int batch, int cap, int Hq);
 hipError_t launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths,
                          bool f32, int batch, int cap, int Hq, int Hkv, float scale, void* out,
                          void* workspace, hipStream_t stream, const void* k_new,
@@ -73,7 +72,7 @@ int mf_decode_static(const void* q, const void* k_cache, const void* v_cache,
   if (int rc = mf::abi_check_decode_shape(dtype, batch, capacity, q_heads, kv_heads, head_dim))
     return rc;
   const bool f32 = dtype == MF_DTYPE_F32;
-  const size_t need = mf::decode_workspace_bytes(batch, capacity, q_heads, mf::decode_chunk(f32));
+  const size_t need = mf::decode_workspace_bytes_any(batch, capacity, q_heads);
   if (need > kScratchBytes)
     return mf::abi_fail(MF_ERR_WORKSPACE,
                         "mf_decode_static needs %zu bytes of scratch; the static array holds %zu "

@@ -18,8 +18,8 @@ from mfattn import _lib, ops
 
 def test_oversized_calls_are_rejected_before_any_launch():
     cap = _lib.LIB.mf_static_scratch_bytes()
-    assert cap == 16 << 20
-    # bf16, 64 rows x 8192 slots x 16 heads needs ~8.7 MB and fits; 256 rows do not
+    assert cap == 32 << 20
+    # 64 rows x 8192 slots x 16 heads need ~17.3 MB and fit; 256 rows do not
     rc = _lib.LIB.mf_decode_static(None, None, None, None, _lib.DTYPE_BF16, 256, 8192, 16, 8, 64,
                                    0.125, None, None)
     assert rc == _lib.ERR_WORKSPACE
