@@ -31,7 +31,8 @@
 
 The decode, the rows and C3/C5 are measured before the C2 step, so the GPU's
 clocks are at their steady state when the headline is timed.
-``--config C3`` or ``--config C5`` prints one of those step lines alone.
+``--config C3`` or ``--config C5`` (or ``--config C2 --step-only``) prints one of
+those step lines alone.
 
 Only one GPU is used; ``--gpus`` above 1 exits with a message.
 """
@@ -418,9 +419,10 @@ TRAFFIC_KERNELS = {
     "attn_fwd": (("mf::attn_fwd_bf16_kernel<",), "C2", None),
     "attn_bwd_dq": (("mf::bwd_dq_bf16_kernel<",), "C2", None),  # computes D itself in the product call
     "attn_bwd_dkdv": (("mf::bwd_dkdv_bf16_kernel<",), "C2", None),
-    "decode": (("mf::decode_prep_kernel", "mf::decode_bf16_kernel<", "mf::decode_combine_kernel<"),
-               "C4", 0),
-    "decode_append": (("mf::decode_bf16_kernel<", "mf::decode_combine_kernel<"), "C4", 1),
+    "decode": (("mf::decode_prep_kernel", "mf::decode_rows_kernel<", "mf::decode_bf16_kernel<",
+                "mf::decode_combine_kernel<"), "C4", 0),
+    "decode_append": (("mf::decode_rows_kernel<", "mf::decode_bf16_kernel<",
+                       "mf::decode_combine_kernel<"), "C4", 1),
     "qk_norm_rope": (("mf::qk_norm_rope_kernel<",), "C2", None),
     "segmented_conv": (("mf::segmented_conv_kernel<",), "C2", None),
 }
@@ -498,6 +500,9 @@ def main() -> int:
     ap.add_argument("--config", default="C2", choices=("C2", "C3", "C5"),
                     help="packed workload of the step (C2, the default, is the headline line with "
                          "the decode, the rows and the CPU baseline; C3 and C5 print the step alone)")
+    ap.add_argument("--step-only", action="store_true",
+                    help="time only the --config step and print its line (no decode, rows, other "
+                         "configs or CPU baseline): the command the per-config kernel traces use")
     ap.add_argument("--profile-step", action="store_true",
                     help="run the calibration copy, one C2 step, one C4 decode and the rows once "
                          "(for rocprofv3 --pmc)")
@@ -514,7 +519,7 @@ def main() -> int:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
               "(the packed-attention path has no cross-GPU work in this build)", file=sys.stderr)
         return 2
-    if args.config != "C2":
+    if args.config != "C2" or args.step_only:
         gpu = gpu_leg(args.steps, args.warmup, name=args.config, decode=False)
         print(json.dumps({"metric": METRIC.split(";")[0], "value": gpu["value"], "unit": "TFLOP/s",
                           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
