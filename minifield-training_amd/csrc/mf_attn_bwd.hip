@@ -713,49 +713,8 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   const bool qvalid = qpos < a.T;
   const bool qactive = qvalid && myqid != 0;
 
-  bf16x8 qf[4], gf[4];
-  {
-    const size_t row = (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
-    const bf16* qs = reinterpret_cast<const bf16*>(a.q) + row;
-    const bf16* gs = reinterpret_cast<const bf16*>(a.dout) + row;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      qf[ks] = ld_bf16x8(qs + ks * 16);
-      gf[ks] = ld_bf16x8(gs + ks * 16);
-    }
-  }
-  const size_t li = ((size_t)b * a.Hq + head) * a.T + min(qpos, a.T - 1);
-  const float lse_raw = a.lse[li];
-  float dlt_raw;
-  if (a.fuse_delta) {
-    // D = rowsum(dO * O): this lane holds half of the row's 64 dims
-    const bf16* os = reinterpret_cast<const bf16*>(a.out) +
-                     (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
-    float part = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const u32x4 ow = ld_u32x4(os + ks * 16);
-      const u32x4 gw = __builtin_bit_cast(u32x4, gf[ks]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // through scalars: __builtin_bit_cast of a vector element reads
-        // element 0 whatever the index (clang 22)
-        const uint32_t oj = ow[j], gj = gw[j];
-        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, oj),
-                                               __builtin_bit_cast(bf16x2, gj), part, false);
-      }
-    }
-    dlt_raw = halves_sum(part);
-    if (qvalid && half == 0) {
-      a.ndelta[li] = -dlt_raw;
-      a.lse2[li] = lse_raw * kLog2e;
-    }
-  } else {
-    dlt_raw = -a.ndelta[li];
-  }
-  drain_memory();
-  const float lse2 = qactive ? lse_raw * kLog2e : kPosInf;
-  const float dlt = qactive ? dlt_raw : 0.f;
+  bf16x8 qf[4], gf[4];  // query and output-gradient fragments (loaded below)
+  float lse2 = 0.f, dlt = 0.f;
   f32x16 dqacc[2] = {zero16(), zero16()};
   const float c = a.scale_log2;
 
@@ -851,11 +810,57 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     if (2 * i + 1 < nsteps) issue(2 * i + 1, slot + kStageBytes);
   };
   const int nslots = (nsteps + 1) >> 1;
+  // Both slots and the query-side rows (q, dO, lse, O for D) are in flight
+  // together before the first wait; after that slot i+1's DMAs are issued
+  // when slot i opens.
   issue_slot(0, slotA);
+  issue_slot(1, slotB);
+  {
+    const size_t row = (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
+    const bf16* qs = reinterpret_cast<const bf16*>(a.q) + row;
+    const bf16* gs = reinterpret_cast<const bf16*>(a.dout) + row;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      qf[ks] = ld_bf16x8(qs + ks * 16);
+      gf[ks] = ld_bf16x8(gs + ks * 16);
+    }
+  }
+  const size_t li = ((size_t)b * a.Hq + head) * a.T + min(qpos, a.T - 1);
+  const float lse_raw = a.lse[li];
+  float dlt_raw;
+  if (a.fuse_delta) {
+    // D = rowsum(dO * O): this lane holds half of the row's 64 dims
+    const bf16* os = reinterpret_cast<const bf16*>(a.out) +
+                     (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
+    float part = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4 ow = ld_u32x4(os + ks * 16);
+      const u32x4 gw = __builtin_bit_cast(u32x4, gf[ks]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // through scalars: __builtin_bit_cast of a vector element reads
+        // element 0 whatever the index (clang 22)
+        const uint32_t oj = ow[j], gj = gw[j];
+        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, oj),
+                                               __builtin_bit_cast(bf16x2, gj), part, false);
+      }
+    }
+    dlt_raw = halves_sum(part);
+    if (qvalid && half == 0) {
+      a.ndelta[li] = -dlt_raw;
+      a.lse2[li] = lse_raw * kLog2e;
+    }
+  } else {
+    dlt_raw = -a.ndelta[li];
+  }
+  drain_memory();
+  lse2 = qactive ? lse_raw * kLog2e : kPosInf;
+  dlt = qactive ? dlt_raw : 0.f;
   for (int i = 0; i < nslots; i += 2) {
     wait_vmcnt<0>();
     barrier();
-    issue_slot(i + 1, slotB);
+    if (i > 0) issue_slot(i + 1, slotB);
     compute(2 * i, slotA);
     if (2 * i + 1 < nsteps) compute(2 * i + 1, slotA + kStageBytes);
     wait_vmcnt<0>();
