@@ -254,9 +254,9 @@ def _time_batch(fn, iters: int) -> float:
 def rows_leg(steps: int, profile: bool = False):
     """The kernels on either side of the attention path at the bench shapes.
 
-    qk_norm_rope, segment_positions and segmented_conv run on the C2 layout
-    (8 x 4096 packed tokens, 16/8 heads of 64, an encoder conv over 1024
-    channels), decode_append on C4 (each row appends at its cache length, then
+    qk_norm_rope, segment_positions and segmented_conv (and the backward of
+    the prologue and the conv) run on the C2 layout (8 x 4096 packed tokens,
+    16/8 heads of 64, an encoder conv over 1024 channels), decode_append on C4 (each row appends at its cache length, then
     decodes), block_map_placements on the placements of C2's segments.
     ``bytes`` counts each input read and each output written once.
     """
@@ -300,7 +300,19 @@ def rows_leg(steps: int, profile: bool = False):
     run("qk_norm_rope", lambda: _lib.check(L.mf_qk_norm_rope(
         p(q), p(k), p(qg), p(kg), p(pos), _lib.DTYPE_BF16, b, t, w.q_heads, w.kv_heads, w.head_dim,
         1e-5, 1e6, p(qo), p(ko), stream)), 2 * (q.nbytes + k.nbytes) + pos.nbytes)
-    del q, k, qo, ko
+    # backward: reads q, k and the output gradients, writes dq, dk (the gain
+    # gradients are reduced through a [blocks, 2, D] fp32 workspace)
+    dqo, dko = torch.randn_like(q), torch.randn_like(k)
+    dqi, dki = torch.empty_like(q), torch.empty_like(k)
+    dgq = torch.empty(w.head_dim, device=dev, dtype=torch.float32)
+    dgk = torch.empty_like(dgq)
+    rws_bytes = L.mf_qk_norm_rope_bwd_workspace_bytes(b, t)
+    rws = torch.empty(max(rws_bytes, 1), dtype=torch.uint8, device=dev)
+    run("qk_norm_rope_bwd", lambda: _lib.check(L.mf_qk_norm_rope_bwd(
+        p(q), p(k), p(qg), p(kg), p(pos), p(dqo), p(dko), _lib.DTYPE_BF16, b, t, w.q_heads,
+        w.kv_heads, w.head_dim, 1e-5, 1e6, p(dqi), p(dki), p(dgq), p(dgk), p(rws), rws_bytes,
+        stream)), 3 * (q.nbytes + k.nbytes) + pos.nbytes)
+    del q, k, qo, ko, dqo, dko, dqi, dki, rws
     ch, taps = 1024, 3
     x = [torch.randn(b, t, ch, generator=g, device=dev).to(bf) for _ in range(3)]
     wt = (0.5 * torch.randn(ch, taps, generator=g, device=dev)).to(bf)
@@ -308,7 +320,18 @@ def rows_leg(steps: int, profile: bool = False):
     run("segmented_conv", lambda: _lib.check(L.mf_segmented_conv(
         p(x[0]), p(x[1]), p(x[2]), p(wt), p(seg), _lib.CONV_CENTERED, _lib.DTYPE_BF16, b, t, ch, taps,
         p(y), stream)), 4 * y.nbytes + seg.nbytes + wt.nbytes)
-    del x, y
+    # backward: reads the gates, the values and dy, writes their three
+    # gradients; the tap gradients go through a per-tile fp32 workspace
+    dx = [torch.empty_like(y) for _ in range(3)]
+    dw = torch.empty(ch, taps, device=dev, dtype=torch.float32)
+    cws_bytes = L.mf_segmented_conv_bwd_workspace_bytes(b, t, ch, taps)
+    cws = torch.empty(max(cws_bytes, 1), dtype=torch.uint8, device=dev)
+    dy = torch.randn_like(y)
+    run("segmented_conv_bwd", lambda: _lib.check(L.mf_segmented_conv_bwd(
+        p(x[0]), p(x[1]), p(x[2]), p(wt), p(seg), p(dy), _lib.CONV_CENTERED, _lib.DTYPE_BF16, b, t,
+        ch, taps, p(dx[0]), p(dx[1]), p(dx[2]), p(dw), p(cws), cws_bytes, stream)),
+        7 * y.nbytes + seg.nbytes + wt.nbytes)
+    del x, y, dx, dy, cws
     runs = []
     for r in range(b):
         ids = w.segment_ids[r]
