@@ -117,3 +117,29 @@ def check_bf16_sum(label: str, a, r, abs_sum, tol: float = BF16_TOL) -> float:
     say(f"{label}: max-abs {diff.max().item():.3e} beyond-rounding {excess:.3e}")
     assert excess < tol, (label, diff.max().item(), excess)
     return excess
+
+
+def short_segment_rows(rng, t: int) -> np.ndarray:
+    """Rows of short segments: increasing ids, runs of 1-128 tokens with and without gaps,
+    128-token runs on and across tile edges next to a single token, and a 200-token run."""
+    rows = []
+    for gaps in (True, False):
+        seg = np.zeros(t, np.int32)
+        pos, sid = 0, int(rng.integers(-6, 0))
+        while pos < t:
+            if gaps and rng.random() < 0.25:
+                pos += int(rng.integers(1, 12))
+                continue
+            n = int(rng.integers(1, 129))
+            sid += int(rng.integers(1, 4))
+            sid += sid == 0
+            seg[pos:pos + n] = sid
+            pos += n
+        rows.append(seg)
+    edge = np.zeros(t, np.int32)
+    edge[:128], edge[128:256], edge[300:428], edge[428:429] = 1, 2, 3, 4
+    rows.append(edge)
+    bad = np.zeros(t, np.int32)
+    bad[10:210], bad[210:260] = 7, 8
+    rows.append(bad)
+    return np.stack(rows)[:, :t]

@@ -15,7 +15,8 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import BF16_TOL, DT, check_bf16, max_abs, operands, say, torch_reference
+from _helpers import (BF16_TOL, DT, check_bf16, max_abs, operands, say, short_segment_rows,
+                      torch_reference)
 from mfattn import _lib, ops
 from mfattn.kernels import attention, bidirectional
 from oracle import attention as oatt
@@ -170,6 +171,43 @@ def test_gqa_ratios(hq, hkv, dtype, mode, device):
             check_bf16(f"gqa {hq}/{hkv} mode {mode} {name}", a, r)
 
 
+@pytest.mark.parametrize("hq, hkv", [(4, 2), (3, 1), (8, 8), (16, 2)])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_short_segment_rows_backward(hq, hkv, mode, device):
+    """bf16 rows of short segments (gaps, single tokens, 128-token runs on and across tile
+    edges, a ragged end) and a row with a longer run, in one batch, against the FP64
+    oracle; the fused call and the phase entry points agree, and a second call is
+    bit-identical."""
+    rng = np.random.default_rng(hq * 3 + hkv + mode)
+    t = 517
+    seg = short_segment_rows(rng, t)
+    say("short-segment rows", hq, hkv, "mode", mode)
+    q, k, v, do = operands(rng, seg.shape[0], t, hq, hkv, 64, torch.bfloat16, 0.5)
+    ts = torch.tensor(seg, device=device)
+    if mode == 0:
+        fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, ts != 0, ts)  # noqa: E731
+    else:
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, ts != 0, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = oatt.grouped_fp64(mode, *(x.float().cpu().numpy() for x in (q, k, v)), seg != 0, seg,
+                            d_out=do.float().cpu().numpy())
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        check_bf16(f"short segments {hq}/{hkv} mode {mode} {name}", a, r)
+    plan = ops.block_map(ts, ts != 0, mode, t, t)
+    out, lse = ops.attn_fwd(q, k, v, plan, mode, 0.125)
+    fused = ops.attn_bwd(q, k, v, out, do, lse, plan, mode, 0.125)
+    ws = ops.bwd_workspace(q)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ops.attn_bwd_delta(out, do, lse, ws)
+    ops.attn_bwd_dq(q, k, v, do, lse, plan, mode, 0.125, ws, dq)
+    ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, 0.125, ws, dk, dv)
+    for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), fused):
+        check_bf16(f"short segments phases vs fused {name}", a, r)
+    again = ops.attn_bwd(q, k, v, out, do, lse, plan, mode, 0.125)
+    for a, r in zip(again, fused):
+        assert torch.equal(a, r)
+
+
 @pytest.mark.parametrize("name", ["C2", "C3", "C5"])
 def test_baseline_config_bf16_fwd_bwd(name, device):
     """Full BASELINE shapes against the fp32 per-segment torch reference."""
@@ -249,14 +287,18 @@ def test_all_padding_rows_and_single_token_segments(device):
         assert (got[0][0] == 0).all() and (got[3][0] == 0).all()
 
 
-def test_deterministic_bitwise(device):
-    w = packing.make_workload("C2")
-    say("determinism C2")
+@pytest.mark.parametrize("name", ["C2", "C5"])
+def test_deterministic_bitwise(name, device):
+    w = packing.make_workload(name)
+    say("determinism", name)
     rng = np.random.default_rng(9)
     q, k, v, do = operands(rng, w.batch, w.length, w.q_heads, w.kv_heads, 64, torch.bfloat16, 0.5)
     tm = torch.tensor(w.attention_mask, device=device)
     ts = torch.tensor(w.segment_ids, device=device)
-    fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    if w.causal:
+        fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+    else:
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
     first = _grads(fn, q, k, v, do)
     second = _grads(fn, q, k, v, do)
     for a, b in zip(first, second):
@@ -282,11 +324,12 @@ def test_head_dim_padding_path(device):
             torch.zeros(1, 8, 2, 128, device=device), ts[:1, :8] * 0 + 1, ts[:1, :8] * 0 + 1)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_phase_entry_points_match_the_fused_backward(dtype, device):
+@pytest.mark.parametrize("dtype, name", [(torch.bfloat16, "C2"), (torch.bfloat16, "C5"),
+                                         (torch.float32, "C1")])
+def test_phase_entry_points_match_the_fused_backward(dtype, name, device):
     """mf_attn_bwd_delta / _dq / _dkdv in sequence give the fused backward's gradients, and the
     delta phase leaves -rowsum(dO * O) and lse * log2(e) in the workspace."""
-    w = packing.make_workload("C1") if dtype == torch.float32 else packing.make_workload("C2")
+    w = packing.make_workload(name)
     say(f"phase entry points {w.name} {dtype}")
     rng = np.random.default_rng(13)
     q, k, v, do = operands(rng, w.batch, w.length, w.q_heads, w.kv_heads, 64, dtype, 0.5)
