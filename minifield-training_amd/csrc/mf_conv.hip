@@ -217,12 +217,11 @@ __global__ __launch_bounds__(256) void segmented_conv_kernel(ConvArgs a) {
 //   db = du * v,  dv = du * b,  dw_i = sum_{b,t} h[t] u[t + o_i] keep(t, t + o_i)
 // in fp32 from the tensor-dtype operands (u and m rounded as the forward
 // rounds them), each gradient rounded once.  Thread = (row, 8 channels, 32
-// output tokens); a workgroup holds 8 channel chunks x 32 token tiles, so the
-// tap-gradient terms of its 32 tiles are added inside it (lanes, then waves)
-// and written as one partial per (workgroup row, channel, tap); a second
-// launch adds the partials in order (deterministic, no atomics).  Neighbour
-// tokens are re-read through the cache, not from HBM: a thread's loads walk
-// 32 + K - 1 consecutive token rows.
+// output tokens), streaming its input rows once through a register ring; a
+// workgroup holds 8 channel chunks x 32 token tiles, so the tap-gradient
+// terms of its 32 tiles are added inside it (lanes, then waves) and written
+// as one partial per (workgroup row, channel, tap); a second launch adds the
+// partials in a fixed order (deterministic, no atomics).
 // ---------------------------------------------------------------------------
 struct ConvBwdArgs {
   const void* b;
@@ -238,6 +237,7 @@ struct ConvBwdArgs {
   int B, T, C, K, centered;
 };
 
+constexpr int kConvBwdTile = 32;    // output tokens per thread of the backward
 constexpr int kConvBwdTiles = 32;   // token tiles per workgroup
 constexpr int kConvBwdChunks = 8;   // 8-channel chunks per workgroup
 
@@ -266,12 +266,112 @@ __device__ __forceinline__ void store8(T* p, const float (&x)[8]) {
   }
 }
 
-template <typename T, int K>
-__global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) {
+// One thread's output tokens t0 .. t0 + kConvBwdTile - 1 for tap offsets
+// LO .. LO + K - 1.  m[t] reads u at t + LO + i and du[t] reads h at
+// t - LO - i, so output t needs input tokens t + SMIN .. t + SMAX.  Input q
+// (token t0 + SMIN + q) goes to ring slot q % R (R = W + kAhead, W the window
+// width) kAhead steps before it is used; at step q output q - (W - 1) is
+// formed from the W newest slots, so every row is loaded once per thread.
+// The step loop is unrolled by R, so all slot indices are compile-time.
+template <typename T, int K, int LO>
+__device__ __forceinline__ void conv_bwd_tile(const ConvBwdArgs& a, size_t row, int t0, int c0,
+                                              const float (&w)[K][8], float (&dw)[K][8]) {
   constexpr bool kBf16 = !std::is_same<T, float>::value;
+  constexpr int SMIN = LO < -LO - (K - 1) ? LO : -LO - (K - 1);
+  constexpr int SMAX = LO + K - 1 > -LO ? LO + K - 1 : -LO;
+  constexpr int W = SMAX - SMIN + 1;
+  constexpr int kAhead = 1;
+  constexpr int R = W + kAhead;
+  constexpr int kSteps = kConvBwdTile + W - 1;
+  const T* vp = reinterpret_cast<const T*>(a.v);
+  const T* bp = reinterpret_cast<const T*>(a.b);
+  const T* cp = reinterpret_cast<const T*>(a.c);
+  const T* gp = reinterpret_cast<const T*>(a.g);
+  Raw8<T> rv[R], rb[R], rg[R], rc[R];
+  int sg[R];
+  auto issue = [&](int q, int slot) {
+    const int s = t0 + SMIN + q;
+    const int sc = min(max(s, 0), a.T - 1);
+    const size_t off = (row + sc) * a.C + c0;
+    rv[slot].load(vp + off);
+    if (a.b) rb[slot].load(bp + off);
+    rg[slot].load(gp + off);
+    if (a.c) rc[slot].load(cp + off);
+    sg[slot] = s != sc ? 0 : a.seg ? a.seg[row + sc] : 1;
+  };
+#pragma unroll
+  for (int q = 0; q < kAhead; ++q) issue(q, q);
+  const int tend = min(kConvBwdTile, a.T - t0);
+#pragma unroll 1
+  for (int q0 = 0; q0 < kSteps; q0 += R) {
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const int q = q0 + k;
+      if (q >= kSteps) break;
+      // the slot of input q - W left the window last step
+      if (q + kAhead < kSteps) issue(q + kAhead, (k + kAhead) % R);
+      const int j = q - (W - 1);
+      if (j < 0 || j >= tend) continue;
+      auto slot = [&](int d) { return ((k - SMAX + d) % R + R) % R; };  // input at t + d
+      const int s0 = slot(0);
+      const int me = sg[s0];
+      float m[8], du[8], h0[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        m[e] = 0.f;
+        du[e] = 0.f;
+        h0[e] = a.c ? rg[s0][e] * rc[s0][e] : rg[s0][e];
+      }
+#pragma unroll
+      for (int i = 0; i < K; ++i) {
+        // forward tap: u at t + LO + i feeds m[t] (rounded in tap order as
+        // the forward does); transposed tap: h at t - LO - i feeds du[t]
+        const int su = slot(LO + i), sh = slot(-LO - i);
+        if (me != 0 && sg[su] == me) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float u = rv[su][e];
+            if (a.b) u = kBf16 ? round_bf16(u * rb[su][e]) : u * rb[su][e];
+            const float p = u * w[i][e];
+            m[e] = kBf16 ? round_bf16(round_bf16(p) + m[e]) : m[e] + p;
+            dw[i][e] = fmaf(h0[e], u, dw[i][e]);
+          }
+        }
+        if (me != 0 && sg[sh] == me) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float hn = a.c ? rg[sh][e] * rc[sh][e] : rg[sh][e];
+            du[e] = fmaf(hn, w[i][e], du[e]);
+          }
+        }
+      }
+      const size_t off = (row + t0 + j) * a.C + c0;
+      if (a.dc) {
+        float dc[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dc[e] = rg[s0][e] * m[e];
+        store8<T>(reinterpret_cast<T*>(a.dc) + off, dc);
+      }
+      float dv[8];
+      if (a.b) {
+        float db[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dv[e] = du[e] * rb[s0][e], db[e] = du[e] * rv[s0][e];
+        store8<T>(reinterpret_cast<T*>(a.db) + off, db);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dv[e] = du[e];
+      }
+      store8<T>(reinterpret_cast<T*>(a.dv) + off, dv);
+    }
+  }
+}
+
+template <typename T, int K, bool CENTERED>
+__global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) {
   __shared__ float red[4][kConvBwdChunks][K * 8];
   const int chunks = a.C / 8;
-  const int tiles = (a.T + kConvTile - 1) / kConvTile;
+  const int tiles = (a.T + kConvBwdTile - 1) / kConvBwdTile;
   const int cgroups = (chunks + kConvBwdChunks - 1) / kConvBwdChunks;
   const int tgroups = (tiles + kConvBwdTiles - 1) / kConvBwdTiles;
   const int cg = blockIdx.x % cgroups;
@@ -282,12 +382,7 @@ __global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) 
   const int tile = tg * kConvBwdTiles + lt;
   const bool on = ch < chunks && tile < tiles;
   const int c0 = min(ch, chunks - 1) * 8;
-  const int lo = a.centered ? -(K / 2) : -(K - 1);
   const size_t row = (size_t)b * a.T;
-  const T* vp = reinterpret_cast<const T*>(a.v);
-  const T* bp = reinterpret_cast<const T*>(a.b);
-  const T* cp = reinterpret_cast<const T*>(a.c);
-  const T* gp = reinterpret_cast<const T*>(a.g);
 
   float w[K][8];
 #pragma unroll
@@ -300,85 +395,9 @@ __global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) 
 #pragma unroll
     for (int e = 0; e < 8; ++e) dw[i][e] = 0.f;
 
-  auto seg_of = [&](int s) { return (s < 0 || s >= a.T) ? 0 : a.seg ? a.seg[row + s] : 1; };
-  // u = b * v at token s (rounded as the forward rounds it), 0 outside the row
-  auto load_u = [&](int s, float (&u)[8]) {
-    const int sc = min(max(s, 0), a.T - 1);
-    load8<T>(vp + (row + sc) * a.C + c0, u);
-    if (a.b) {
-      float bb[8];
-      load8<T>(bp + (row + sc) * a.C + c0, bb);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) u[e] = kBf16 ? round_bf16(u[e] * bb[e]) : u[e] * bb[e];
-    }
-  };
-  // h = g * c at token s
-  auto load_h = [&](int s, float (&h)[8]) {
-    const int sc = min(max(s, 0), a.T - 1);
-    load8<T>(gp + (row + sc) * a.C + c0, h);
-    if (a.c) {
-      float cc[8];
-      load8<T>(cp + (row + sc) * a.C + c0, cc);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) h[e] *= cc[e];
-    }
-  };
-
   if (on) {
-    const int t0 = tile * kConvTile;
-    const int tend = min(t0 + kConvTile, a.T);
-    for (int t = t0; t < tend; ++t) {
-      const int me = seg_of(t);
-      const size_t off = (row + t) * a.C + c0;
-      float h[8], m[8], du[8];
-      load_h(t, h);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) m[e] = 0.f, du[e] = 0.f;
-#pragma unroll
-      for (int i = 0; i < K; ++i) {
-        // forward tap: u at t + o_i feeds m[t] (rounded in tap order as the
-        // forward does); transposed tap: h at t - o_i feeds du[t]
-        const int s_fwd = t + lo + i, s_bwd = t - lo - i;
-        const bool keep_fwd = me != 0 && seg_of(s_fwd) == me;
-        const bool keep_bwd = me != 0 && seg_of(s_bwd) == me;
-        if (keep_fwd) {
-          float u[8];
-          load_u(s_fwd, u);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float p = u[e] * w[i][e];
-            m[e] = kBf16 ? round_bf16(round_bf16(p) + m[e]) : m[e] + p;
-            dw[i][e] = fmaf(h[e], u[e], dw[i][e]);
-          }
-        }
-        if (keep_bwd) {
-          float hn[8];
-          load_h(s_bwd, hn);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) du[e] = fmaf(hn[e], w[i][e], du[e]);
-        }
-      }
-      if (a.dc) {
-        float gg[8], dc[8];
-        load8<T>(gp + off, gg);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dc[e] = gg[e] * m[e];
-        store8<T>(reinterpret_cast<T*>(a.dc) + off, dc);
-      }
-      float vv[8], dv[8];
-      if (a.b) {
-        float bb[8], db[8];
-        load8<T>(bp + off, bb);
-        load8<T>(vp + off, vv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dv[e] = du[e] * bb[e], db[e] = du[e] * vv[e];
-        store8<T>(reinterpret_cast<T*>(a.db) + off, db);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) dv[e] = du[e];
-      }
-      store8<T>(reinterpret_cast<T*>(a.dv) + off, dv);
-    }
+    const int t0 = tile * kConvBwdTile;
+    conv_bwd_tile<T, K, CENTERED ? -(K / 2) : -(K - 1)>(a, row, t0, c0, w, dw);
   }
   // tap gradients: add the 8 tiles of each wave (lanes lc, lc + 8, ... hold
   // the same channels), then the 4 waves, in a fixed order
@@ -403,18 +422,31 @@ __global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) 
   }
 }
 
-// d taps [C][K] fp32: the partials of every (row, tile group) added in order.
-__global__ __launch_bounds__(256) void conv_taps_reduce_kernel(const float* partials, int parts,
-                                                               int n, float* dw) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= n) return;
+// d taps [C][K] fp32: the partials of every (row, tile group) added in a
+// fixed order.  A block takes 32 columns; thread (slice, column) adds parts
+// slice, slice + 8, ..., and the 8 slice sums are added in slice order.
+constexpr int kTapCols = 32, kTapSlices = 8;
+
+__global__ __launch_bounds__(kTapCols * kTapSlices) void conv_taps_reduce_kernel(
+    const float* partials, int parts, int n, float* dw) {
+  __shared__ float acc_l[kTapSlices][kTapCols];
+  const int c = threadIdx.x % kTapCols, sl = threadIdx.x / kTapCols;
+  const int j = blockIdx.x * kTapCols + c;
   float acc = 0.f;
-  for (int p = 0; p < parts; ++p) acc += partials[(size_t)p * n + j];
-  dw[j] = acc;
+  if (j < n)
+    for (int p = sl; p < parts; p += kTapSlices) acc += partials[(size_t)p * n + j];
+  acc_l[sl][c] = acc;
+  __syncthreads();
+  if (sl == 0 && j < n) {
+    float v = acc_l[0][c];
+#pragma unroll
+    for (int k = 1; k < kTapSlices; ++k) v += acc_l[k][c];
+    dw[j] = v;
+  }
 }
 
 size_t conv_bwd_parts(int B, int T) {
-  const int tiles = (T + kConvTile - 1) / kConvTile;
+  const int tiles = (T + kConvBwdTile - 1) / kConvBwdTile;
   return (size_t)B * ((tiles + kConvBwdTiles - 1) / kConvBwdTiles);
 }
 
@@ -425,19 +457,27 @@ size_t conv_bwd_workspace_bytes(int B, int T, int C, int K) {
 template <typename T>
 hipError_t launch_conv_bwd_t(const ConvBwdArgs& a, hipStream_t stream) {
   const int chunks = a.C / 8;
-  const int tiles = (a.T + kConvTile - 1) / kConvTile;
+  const int tiles = (a.T + kConvBwdTile - 1) / kConvBwdTile;
   const long long blocks = (long long)a.B * ((tiles + kConvBwdTiles - 1) / kConvBwdTiles) *
                            ((chunks + kConvBwdChunks - 1) / kConvBwdChunks);
   const dim3 grid((unsigned)blocks);
+#define MF_CONV_BWD_CASE(KK)                                                                     \
+    case KK:                                                                                      \
+      if (a.centered)                                                                             \
+        hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, KK, true>), grid, dim3(256), 0, stream, a); \
+      else                                                                                        \
+        hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, KK, false>), grid, dim3(256), 0, stream, a); \
+      break;
   switch (a.K) {
-    case 1: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 1>), grid, dim3(256), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 2>), grid, dim3(256), 0, stream, a); break;
-    case 3: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 3>), grid, dim3(256), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 4>), grid, dim3(256), 0, stream, a); break;
-    case 5: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 5>), grid, dim3(256), 0, stream, a); break;
-    case 6: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 6>), grid, dim3(256), 0, stream, a); break;
-    case 7: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 7>), grid, dim3(256), 0, stream, a); break;
-    case 8: hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, 8>), grid, dim3(256), 0, stream, a); break;
+    MF_CONV_BWD_CASE(1)
+    MF_CONV_BWD_CASE(2)
+    MF_CONV_BWD_CASE(3)
+    MF_CONV_BWD_CASE(4)
+    MF_CONV_BWD_CASE(5)
+    MF_CONV_BWD_CASE(6)
+    MF_CONV_BWD_CASE(7)
+    MF_CONV_BWD_CASE(8)
+#undef MF_CONV_BWD_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -466,8 +506,9 @@ hipError_t launch_segmented_conv_bwd(const void* b, const void* c, const void* v
   const hipError_t e = f32 ? launch_conv_bwd_t<float>(a, stream) : launch_conv_bwd_t<bf16>(a, stream);
   if (e != hipSuccess) return e;
   const int n = C * K;
-  hipLaunchKernelGGL(conv_taps_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
-                     a.partials, (int)conv_bwd_parts(B, T), n, dw);
+  hipLaunchKernelGGL(conv_taps_reduce_kernel, dim3((n + kTapCols - 1) / kTapCols),
+                     dim3(kTapCols * kTapSlices), 0, stream, a.partials, (int)conv_bwd_parts(B, T),
+                     n, dw);
   return hipGetLastError();
 }
 

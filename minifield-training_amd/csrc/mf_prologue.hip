@@ -179,80 +179,84 @@ struct RopeBwdArgs {
   float freq[kD / 2];
 };
 
-constexpr int kRopeBwdBlocks = 1024;  // workgroups of the backward (fewer for short inputs)
+constexpr int kRopeBwdBlocks = 2048;  // workgroups of the backward (fewer for short inputs)
+constexpr int kRopeBatch = 2;          // (token, head group) rows loaded before any is computed
+
+// One 8-head group of a token's rows as loaded (16 bytes per lane in bf16,
+// 32 in fp32), kept raw until the group is computed, so that every load of
+// a token is in flight before the first use.
+template <bool F32> struct RopeRow;
+template <> struct RopeRow<false> { bf16x8 v; };
+template <> struct RopeRow<true> { f32x4 a, b; };
 
 template <bool F32>
-__device__ __forceinline__ void norm_rope_rows_bwd(const void* src, const void* gout, void* dst,
-                                                   const void* gain, int H, size_t token,
-                                                   int lane, const float* cs, const float* sn,
-                                                   float eps, float (&dw)[8]) {
-  typedef typename std::conditional<F32, float, bf16>::type T;
-  const int g = lane >> 3, dl = lane & 7;
-  float w[8], c[8], s[8];
+__device__ __forceinline__ RopeRow<F32> load_rope_row(const void* src, size_t base) {
+  RopeRow<F32> r;
+  if constexpr (F32) {
+    const float* p = reinterpret_cast<const float*>(src) + base;
+    r.a = *reinterpret_cast<const f32x4*>(p);
+    r.b = *reinterpret_cast<const f32x4*>(p + 4);
+  } else {
+    r.v = ld_bf16x8(reinterpret_cast<const bf16*>(src) + base);
+  }
+  return r;
+}
+
+template <bool F32>
+__device__ __forceinline__ void rope_row_floats(const RopeRow<F32>& r, float (&x)[8]) {
+  if constexpr (F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = r.a[i], x[4 + i] = r.b[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = (float)r.v[i];
+  }
+}
+
+// The VJP of one loaded group: lane (g, dl) holds dims 8 dl .. 8 dl + 7 of
+// head g.  Every lane takes part (shuffles and the 8-lane sums); only live
+// lanes store and accumulate the gain gradient.
+template <bool F32>
+__device__ __forceinline__ void norm_rope_bwd_store(const RopeRow<F32>& xin,
+                                                    const RopeRow<F32>& gin, void* dst,
+                                                    size_t base, bool live, const float (&w)[8],
+                                                    const float (&c)[8], const float (&s)[8],
+                                                    int dl, float eps, float (&dw)[8]) {
+  float x[8], go[8];
+  rope_row_floats<F32>(xin, x);
+  rope_row_floats<F32>(gin, go);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+  const float inv = rsqrtf(dpp_xor_sum8(ss) * (1.f / kD) + eps);
+  float dy[8], y[8], dot = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int d = 8 * dl + i;
-    w[i] = (float)reinterpret_cast<const T*>(gain)[d];
-    c[i] = cs[d & 31];
-    s[i] = sn[d & 31];
-    if constexpr (!F32) {
-      c[i] = round_bf16(c[i]);
-      s[i] = round_bf16(s[i]);
-    }
+    // rot^T: dims d < 32 take +g[d + 32], dims d >= 32 take -g[d - 32]
+    const float o = __shfl_xor(go[i], 4);
+    const float dn = fmaf(go[i], c[i], (dl < 4 ? o : -o) * s[i]);
+    y[i] = x[i] * inv;
+    const float yr = F32 ? y[i] : round_bf16(y[i]);
+    if (live) dw[i] = fmaf(dn, yr, dw[i]);
+    dy[i] = dn * w[i];
+    dot = fmaf(dy[i], y[i], dot);
   }
-  for (int h0 = 0; h0 < H; h0 += 8) {
-    const int h = h0 + g;
-    const bool live = h < H;
-    const size_t base = (token * H + min(h, H - 1)) * kD + 8 * dl;
-    float x[8], go[8];
-    if constexpr (F32) {
-      const float* xs = reinterpret_cast<const float*>(src) + base;
-      const float* gs = reinterpret_cast<const float*>(gout) + base;
-      const f32x4 a = *reinterpret_cast<const f32x4*>(xs);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(xs + 4);
-      const f32x4 ga = *reinterpret_cast<const f32x4*>(gs);
-      const f32x4 gb = *reinterpret_cast<const f32x4*>(gs + 4);
+  const float mean = dpp_xor_sum8(dot) * (1.f / kD);
+  if (!live) return;
+  if constexpr (F32) {
+    f32x4 oa, ob;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i], go[i] = ga[i], go[4 + i] = gb[i];
-    } else {
-      const bf16x8 a = ld_bf16x8(reinterpret_cast<const bf16*>(src) + base);
-      const bf16x8 ga = ld_bf16x8(reinterpret_cast<const bf16*>(gout) + base);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = (float)a[i], go[i] = (float)ga[i];
+    for (int i = 0; i < 4; ++i) {
+      oa[i] = inv * fmaf(-y[i], mean, dy[i]);
+      ob[i] = inv * fmaf(-y[4 + i], mean, dy[4 + i]);
     }
-    float ss = 0.f;
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base) = oa;
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base + 4) = ob;
+  } else {
+    bf16x8 o;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
-    const float inv = rsqrtf(dpp_xor_sum8(ss) * (1.f / kD) + eps);
-    float dy[8], y[8], dot = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      // rot^T: dims d < 32 take +g[d + 32], dims d >= 32 take -g[d - 32]
-      const float o = __shfl_xor(go[i], 4);
-      const float dn = fmaf(go[i], c[i], (dl < 4 ? o : -o) * s[i]);
-      y[i] = x[i] * inv;
-      const float yr = F32 ? y[i] : round_bf16(y[i]);
-      if (live) dw[i] = fmaf(dn, yr, dw[i]);
-      dy[i] = dn * w[i];
-      dot = fmaf(dy[i], y[i], dot);
-    }
-    const float mean = dpp_xor_sum8(dot) * (1.f / kD);
-    if (!live) continue;
-    if constexpr (F32) {
-      f32x4 a, b;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = inv * fmaf(-y[i], mean, dy[i]);
-        b[i] = inv * fmaf(-y[4 + i], mean, dy[4 + i]);
-      }
-      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base) = a;
-      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base + 4) = b;
-    } else {
-      bf16x8 o;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (bf16)(inv * fmaf(-y[i], mean, dy[i]));
-      *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(dst) + base) = o;
-    }
+    for (int i = 0; i < 8; ++i) o[i] = (bf16)(inv * fmaf(-y[i], mean, dy[i]));
+    *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(dst) + base) = o;
   }
 }
 
@@ -267,29 +271,83 @@ __device__ __forceinline__ float heads_sum8(float x) {
 
 template <bool F32>
 __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(RopeBwdArgs a) {
-  __shared__ float cs_l[4][kD / 2], sn_l[4][kD / 2];
   __shared__ float part[4][2][kD];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int g = lane >> 3, dl = lane & 7;
   const size_t total = (size_t)a.B * a.T;
   const size_t stride = (size_t)gridDim.x * 4;
-  float dwq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dwk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  // every wave runs the same number of iterations (tokens past the end redo
-  // the last token and store nothing), so the block-wide barriers match
-  const size_t iters = (total + stride - 1) / stride;
-  for (size_t it = 0; it < iters; ++it) {
-    const size_t token = it * stride + (size_t)blockIdx.x * 4 + wave;
-    const size_t tok = token < total ? token : total - 1;
-    __syncthreads();  // the previous token's angles have been read
-    token_angles(a.positions, tok, a.T, a.freq, lane, cs_l[wave], sn_l[wave]);
-    __syncthreads();
-    if (token >= total) continue;
-    norm_rope_rows_bwd<F32>(a.q, a.dq_out, a.dq, a.q_gain, a.Hq, tok, lane, cs_l[wave],
-                            sn_l[wave], a.eps, dwq);
-    norm_rope_rows_bwd<F32>(a.k, a.dk_out, a.dk, a.k_gain, a.Hkv, tok, lane, cs_l[wave],
-                            sn_l[wave], a.eps, dwk);
+  const int gq = (a.Hq + 7) >> 3;
+  const int groups = gq + ((a.Hkv + 7) >> 3);  // 8-head groups of a token, q first
+  typedef typename std::conditional<F32, float, bf16>::type T;
+  float wq[8], wk[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    wq[i] = (float)reinterpret_cast<const T*>(a.q_gain)[8 * dl + i];
+    wk[i] = (float)reinterpret_cast<const T*>(a.k_gain)[8 * dl + i];
   }
-  const int dl = lane & 7;
+  float dwq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dwk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  // (token, group) of this wave's rows; no barrier inside the loop, so the
+  // waves of a block need not run the same number of tokens
+  auto locate = [&](size_t tok, int i, const void*& src, const void*& gsrc, void*& dst,
+                    size_t& base, bool& live) {
+    const bool isq = i < gq;
+    const int H = isq ? a.Hq : a.Hkv;
+    const int h = 8 * (isq ? i : i - gq) + g;
+    live = h < H;
+    base = (tok * H + min(h, H - 1)) * kD + 8 * dl;
+    src = isq ? a.q : a.k;
+    gsrc = isq ? a.dq_out : a.dk_out;
+    dst = isq ? a.dq : a.dk;
+  };
+  for (size_t tok = (size_t)blockIdx.x * 4 + wave; tok < total; tok += stride) {
+    float c[8], s[8];
+    for (int i0 = 0; i0 < groups; i0 += kRopeBatch) {
+      RopeRow<F32> x[kRopeBatch], go[kRopeBatch];
+#pragma unroll
+      for (int j = 0; j < kRopeBatch; ++j) {
+        if (i0 + j < groups) {
+          const void *src, *gsrc;
+          void* dst;
+          size_t base;
+          bool live;
+          locate(tok, i0 + j, src, gsrc, dst, base, live);
+          x[j] = load_rope_row<F32>(src, base);
+          go[j] = load_rope_row<F32>(gsrc, base);
+        }
+      }
+      if (i0 == 0) {
+        // the token's 32 angles (lanes j and j + 32 compute angle j), read
+        // by each lane for its dims with shuffles; overlaps the loads
+        const float pos = (float)(a.positions ? a.positions[tok] : (int)(tok % a.T));
+        float sv, cv;
+        sincosf(pos * a.freq[lane & 31], &sv, &cv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          c[i] = __shfl(cv, (8 * dl + i) & 31);
+          s[i] = __shfl(sv, (8 * dl + i) & 31);
+          if constexpr (!F32) {
+            c[i] = round_bf16(c[i]);
+            s[i] = round_bf16(s[i]);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kRopeBatch; ++j) {
+        if (i0 + j < groups) {
+          const void *src, *gsrc;
+          void* dst;
+          size_t base;
+          bool live;
+          locate(tok, i0 + j, src, gsrc, dst, base, live);
+          if (i0 + j < gq)
+            norm_rope_bwd_store<F32>(x[j], go[j], dst, base, live, wq, c, s, dl, a.eps, dwq);
+          else
+            norm_rope_bwd_store<F32>(x[j], go[j], dst, base, live, wk, c, s, dl, a.eps, dwk);
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float sq = heads_sum8(dwq[i]), sk = heads_sum8(dwk[i]);
@@ -306,13 +364,25 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(RopeBwdArgs a) {
   }
 }
 
-// dq_gain / dk_gain: the per-workgroup partials added in workgroup order.
-__global__ __launch_bounds__(128) void rope_gain_reduce_kernel(const float* partials, int blocks,
-                                                               float* dq_gain, float* dk_gain) {
-  const int which = threadIdx.x / kD, d = threadIdx.x % kD;
+// Sum of the per-workgroup gain partials in a fixed order: one block per
+// column (2 gains x 64 dims); thread j adds workgroups j, j + 256, ... and
+// the 256 sums are added as a tree in LDS.
+constexpr int kRopeReduceThreads = 256;
+
+__global__ __launch_bounds__(kRopeReduceThreads) void rope_gain_reduce_kernel(
+    const float* partials, int blocks, float* dq_gain, float* dk_gain) {
+  __shared__ float acc_l[kRopeReduceThreads];
+  const int col = blockIdx.x;
   float acc = 0.f;
-  for (int b = 0; b < blocks; ++b) acc += partials[((size_t)b * 2 + which) * kD + d];
-  (which ? dk_gain : dq_gain)[d] = acc;
+  for (int b = threadIdx.x; b < blocks; b += kRopeReduceThreads)
+    acc += partials[(size_t)b * 2 * kD + col];
+  acc_l[threadIdx.x] = acc;
+  __syncthreads();
+  for (int n = kRopeReduceThreads / 2; n > 0; n >>= 1) {
+    if (threadIdx.x < n) acc_l[threadIdx.x] += acc_l[threadIdx.x + n];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) (col >= kD ? dk_gain : dq_gain)[col % kD] = acc_l[0];
 }
 
 // Packer positions from segment ids: the offset of each token inside its run
@@ -414,8 +484,8 @@ hipError_t launch_qk_norm_rope_bwd(const void* q, const void* k, const void* q_g
     hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<true>), dim3(blocks), dim3(256), 0, stream, a);
   else
     hipLaunchKernelGGL((qk_norm_rope_bwd_kernel<false>), dim3(blocks), dim3(256), 0, stream, a);
-  hipLaunchKernelGGL(rope_gain_reduce_kernel, dim3(1), dim3(2 * kD), 0, stream, a.partials,
-                     blocks, dq_gain, dk_gain);
+  hipLaunchKernelGGL(rope_gain_reduce_kernel, dim3(2 * kD), dim3(kRopeReduceThreads), 0, stream,
+                     a.partials, blocks, dq_gain, dk_gain);
   return hipGetLastError();
 }
 
