@@ -216,7 +216,7 @@ __global__ __launch_bounds__(256) void segmented_conv_kernel(ConvArgs a) {
 //   du[s] = sum_i h[s - o_i] w_i keep(s - o_i, s)     (keep is symmetric)
 //   db = du * v,  dv = du * b,  dw_i = sum_{b,t} h[t] u[t + o_i] keep(t, t + o_i)
 // in fp32 from the tensor-dtype operands (u and m rounded as the forward
-// rounds them), each gradient rounded once.  Thread = (row, 8 channels, 32
+// rounds them), each gradient rounded once.  Thread = (row, 8 channels, 16
 // output tokens), streaming its input rows once through a register ring; a
 // workgroup holds 8 channel chunks x 32 token tiles, so the tap-gradient
 // terms of its 32 tiles are added inside it (lanes, then waves) and written
@@ -237,7 +237,7 @@ struct ConvBwdArgs {
   int B, T, C, K, centered;
 };
 
-constexpr int kConvBwdTile = 32;    // output tokens per thread of the backward
+constexpr int kConvBwdTile = 16;    // output tokens per thread of the backward
 constexpr int kConvBwdTiles = 32;   // token tiles per workgroup
 constexpr int kConvBwdChunks = 8;   // 8-channel chunks per workgroup
 

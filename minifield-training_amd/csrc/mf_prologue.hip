@@ -179,7 +179,7 @@ struct RopeBwdArgs {
   float freq[kD / 2];
 };
 
-constexpr int kRopeBwdBlocks = 2048;  // workgroups of the backward (fewer for short inputs)
+constexpr int kRopeBwdBlocks = 1024;  // workgroups of the backward (fewer for short inputs)
 constexpr int kRopeBatch = 2;          // (token, head group) rows loaded before any is computed
 
 // One 8-head group of a token's rows as loaded (16 bytes per lane in bf16,
