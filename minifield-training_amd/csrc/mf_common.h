@@ -85,6 +85,16 @@ __device__ __forceinline__ float round_bf16(float x) {
   return __builtin_bit_cast(float, r << 16);
 }
 
+// x and y rounded to bf16 (nearest even) by one conversion, packed (x in the
+// low half); inline asm for the same reason as round_bf16.
+__device__ __forceinline__ uint32_t round_bf16_pair(float x, float y) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+  return r;
+}
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __builtin_bit_cast(float, u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __builtin_bit_cast(float, u & 0xffff0000u); }
+
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane j receives
 // element e (0..3) = halfword (j & 3) of the 8 bytes addressed by lane
 // (j >> 2) + 4e.  If lane i of the group addresses row base + (i >> 2),

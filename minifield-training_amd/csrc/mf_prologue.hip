@@ -85,13 +85,19 @@ __device__ __forceinline__ void norm_rope_rows(const void* src, void* dst, const
     for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
     const float inv = rsqrtf(dpp_xor_sum8(ss) * (1.f / kD) + eps);
     float n[8], r[8];
+    if constexpr (F32) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = x[i] * inv;
-      if constexpr (!F32) v = round_bf16(v);
-      v *= w[i];
-      if constexpr (!F32) v = round_bf16(v);
-      n[i] = v;
+      for (int i = 0; i < 8; ++i) n[i] = x[i] * inv * w[i];
+    } else {
+      // the normalised value, then its product with the gain, each rounded
+      // to bf16; two elements per conversion
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const uint32_t y = round_bf16_pair(x[i] * inv, x[i + 1] * inv);
+        const uint32_t z = round_bf16_pair(bf16_lo(y) * w[i], bf16_hi(y) * w[i + 1]);
+        n[i] = bf16_lo(z);
+        n[i + 1] = bf16_hi(z);
+      }
     }
     // rotate_half: dims d < 32 take -n[d + 32], dims d >= 32 take n[d - 32]
 #pragma unroll
@@ -110,10 +116,15 @@ __device__ __forceinline__ void norm_rope_rows(const void* src, void* dst, const
       *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base) = a;
       *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base + 4) = b;
     } else {
+      // the two rotation products rounded to bf16 by one conversion and added
+      // by one dot product with (1, 1) (exact products, one fp32 rounding)
+      const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
       bf16x8 o;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        o[i] = (bf16)(round_bf16(n[i] * c[i]) + round_bf16(r[i] * s[i]));
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t pq = round_bf16_pair(n[i] * c[i], r[i] * s[i]);
+        o[i] = (bf16)__builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pq), ones, 0.f, false);
+      }
       *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(dst) + base) = o;
     }
   }
