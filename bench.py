@@ -447,7 +447,11 @@ TRAFFIC_KERNELS = {
     "decode_append": (("mf::decode_rows_kernel<", "mf::decode_bf16_kernel<",
                        "mf::decode_combine_kernel<"), "C4", 1),
     "qk_norm_rope": (("mf::qk_norm_rope_kernel<",), "C2", None),
+    "qk_norm_rope_bwd": (("mf::qk_norm_rope_bwd_kernel<", "mf::rope_gain_reduce_kernel"), "C2",
+                         None),
     "segmented_conv": (("mf::segmented_conv_kernel<",), "C2", None),
+    "segmented_conv_bwd": (("mf::segmented_conv_bwd_kernel<", "mf::conv_taps_reduce_kernel"),
+                           "C2", None),
 }
 
 
