@@ -65,8 +65,11 @@ extern "C" {
  *                             token or padding past the sequence end)
  * [1] kid int32 [B][nK*128]   canonical key ids (same convention)
  * [2] tile map uint8 [B][nQ][nK]
- * [3] q_count int32 [B][nQ]    [4] q_list int32 [B][nQ][nK] (kj*4 + class)
- * [5] k_count int32 [B][nK]    [6] k_list int32 [B][nK][nQ] (qi*4 + class)
+ * [3] q_count int32 [B][nQ]    [4] q_list int32 [B][nQ][2*nK]: the 64-key
+ *                              stages s (keys 64s .. 64s+63) a query tile
+ *                              attends to, as s*4 + class
+ * [5] k_count int32 [B][nK]    [6] k_list int32 [B][nK][2*nQ]: the 64-query
+ *                              stages of a key tile, s*4 + class
  * [7] q_order int32 [B*nQ]     [8] k_order int32 [B*nK]: the items b*nQ + qi
  *                              (b*nK + kj) by decreasing list length, the
  *                              attention kernels' launch order

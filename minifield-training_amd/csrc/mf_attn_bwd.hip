@@ -256,13 +256,13 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
   }
 
   const int count = ld_const(a.qcnt, b * a.nq + qt);
-  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
-  const int nsteps = count * (kTile / kStep);
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * 2 * a.nk;
+  const int nsteps = count;  // one 64-key stage per list entry
   const float c = a.scale_log2;
 
   DqStage<F32> stage;
   if (nsteps > 0) {
-    const int kb0 = (list[0] >> 2) * kTile;
+    const int kb0 = (list[0] >> 2) * kStep;
     dq_load<F32>(a, b, kvh, kb0, stage);
     dq_store<F32>(a, b, kb0, stage, lds, 0);
   }
@@ -270,13 +270,12 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
 
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
-    const int entry = list[step >> 1];
-    const int kb = (entry >> 2) * kTile + (step & 1) * kStep;
+    const int entry = list[step];
+    const int kb = (entry >> 2) * kStep;
     const bool partial = (entry & 3) == 1;
     int next_kb = 0;
     if (step + 1 < nsteps) {
-      const int e2 = list[(step + 1) >> 1];
-      next_kb = (e2 >> 2) * kTile + ((step + 1) & 1) * kStep;
+      next_kb = (list[step + 1] >> 2) * kStep;
       dq_load<F32>(a, b, kvh, next_kb, stage);
     }
 
@@ -428,15 +427,12 @@ struct KvStage {
   int qid;
 };
 
-// Iteration `it` of a key tile's loop -> (query tile entry, head in group,
-// 64-query half).
+// Iteration `it` of a key tile's loop -> (64-query stage entry, head in group).
 __device__ __forceinline__ void kv_iter(const BwdArgs& a, const int* list, int it, int& qb,
                                         int& head_in_group, int& cls) {
-  const int per_tile = a.G * 2;
-  const int entry = list[it / per_tile];
-  const int rem = it % per_tile;
-  head_in_group = rem >> 1;
-  qb = (entry >> 2) * kTile + (rem & 1) * kStep;
+  const int entry = list[it / a.G];
+  head_in_group = it % a.G;
+  qb = (entry >> 2) * kStep;
   cls = entry & 3;
 }
 
@@ -559,8 +555,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
   dkacc[0] = dkacc[1] = dvacc[0] = dvacc[1] = zero16();
 
   const int count = ld_const(a.kcnt, b * a.nk + kt);
-  const int* list = a.klist + ((size_t)b * a.nk + kt) * a.nq;
-  const int niters = count * a.G * 2;
+  const int* list = a.klist + ((size_t)b * a.nk + kt) * 2 * a.nq;
+  const int niters = count * a.G;  // (64-query stage, head) iterations
   const float c = a.scale_log2;
 
   KvStage<F32> stage;
@@ -719,9 +715,9 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   const float c = a.scale_log2;
 
   const int count = ld_const(a.qcnt, b * a.nq + qt);
-  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
-  const int nsteps = count * (kTile / kKvStep);
-  auto step_kb = [&](int s) { return (ld_const(list, s >> 1) >> 2) * kTile + (s & 1) * kKvStep; };
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * 2 * a.nk;
+  const int nsteps = count;  // one 64-key stage per list entry
+  auto step_kb = [&](int s) { return (ld_const(list, s) >> 2) * kKvStep; };
   const int tr_row = tr_row_of(lane);
   const int tr_col = tr_col_of(lane);
   const int* kid_row = a.kid + (size_t)b * a.tk_pad;
@@ -776,8 +772,8 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   };
 
   auto compute = [&](int step, const char* stage) {
-    const int entry = ld_const(list, step >> 1);
-    const int kb = (entry >> 2) * kTile + (step & 1) * kKvStep;
+    const int entry = ld_const(list, step);
+    const int kb = (entry >> 2) * kKvStep;
     const bool partial = (entry & 3) == 1;
     const char* kt = stage;
     const char* vt = stage + kTileBytes;
@@ -950,10 +946,9 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   f32x16 dkacc[2] = {zero16(), zero16()}, dvacc[2] = {zero16(), zero16()};
 
   const int count = ld_const(a.kcnt, b * a.nk + kt);
-  const int* list = a.klist + ((size_t)b * a.nk + kt) * a.nq;
+  const int* list = a.klist + ((size_t)b * a.nk + kt) * 2 * a.nq;
   const int hps = a.G / HS;        // heads per slot
-  const int per_tile = hps * 2;    // (head, 64-query half) iterations per query tile
-  const int niters = count * per_tile;
+  const int niters = count * hps;  // (64-query stage, head) iterations
   const float c = a.scale_log2;
   const uint32_t qrow_stride = (uint32_t)a.Hq * kD * sizeof(bf16);
 
@@ -963,10 +958,9 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   // DMA of iteration `it` (query rows qb .. qb+63 of HS heads) into a stage.
   auto issue = [&](int it, char* stage) {
     it = min(it, niters - 1);
-    const int entry = ld_const(list, it / per_tile);
-    const int rem = it % per_tile;
-    const int hj = rem >> 1;
-    const int qb = (entry >> 2) * kTile + (rem & 1) * kKvStep;
+    const int entry = ld_const(list, it / hps);
+    const int hj = it % hps;
+    const int qb = (entry >> 2) * kKvStep;
     // the word arrays first, so the short step wait covers them
     if (wave < Q::kWordArrays) {
       // rows past T re-read row T-1 (finite values); their ids are 0, so
@@ -1078,9 +1072,8 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   };
 
   auto compute = [&](int it, const char* stage) {
-    const int entry = ld_const(list, it / per_tile);
-    const int rem = it % per_tile;
-    const int qb = (entry >> 2) * kTile + (rem & 1) * kKvStep;
+    const int entry = ld_const(list, it / hps);
+    const int qb = (entry >> 2) * kKvStep;
     const bool partial = (entry & 3) == 1;
     const char* qt = stage + 2 * slot * kTileBytes;
     const char* gt = stage + (2 * slot + 1) * kTileBytes;

@@ -201,27 +201,26 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
   }
 
   const int count = ld_const(a.qcnt, b * a.nq + qt);
-  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
-  const int nsteps = count * (kTile / kStepK);
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * 2 * a.nk;
+  const int nsteps = count;  // one 64-key stage per list entry
   const float c = a.scale_log2;
 
   FwdStage<F32> stage;
   if (nsteps > 0) {
     const int e0 = list[0];
-    fwd_load<F32>(a, b, kvh, (e0 >> 2) * kTile, stage);
-    fwd_store<F32>(a, b, (e0 >> 2) * kTile, stage, lds, 0);
+    fwd_load<F32>(a, b, kvh, (e0 >> 2) * kStepK, stage);
+    fwd_store<F32>(a, b, (e0 >> 2) * kStepK, stage, lds, 0);
   }
   __syncthreads();
 
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
-    const int entry = list[step >> 1];
-    const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
+    const int entry = list[step];
+    const int kb = (entry >> 2) * kStepK;
     const bool partial = (entry & 3) == 1;
     int next_kb = 0;
     if (step + 1 < nsteps) {
-      const int e2 = list[(step + 1) >> 1];
-      next_kb = (e2 >> 2) * kTile + ((step + 1) & 1) * kStepK;
+      next_kb = (list[step + 1] >> 2) * kStepK;
       fwd_load<F32>(a, b, kvh, next_kb, stage);
     }
 
@@ -428,9 +427,9 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   const float c = a.scale_log2;
 
   const int count = ld_const(a.qcnt, b * a.nq + qt);
-  const int* list = a.qlist + ((size_t)b * a.nq + qt) * a.nk;
-  const int nsteps = count * (kTile / kStepK);
-  auto step_kb = [&](int s) { return (ld_const(list, s >> 1) >> 2) * kTile + (s & 1) * kStepK; };
+  const int* list = a.qlist + ((size_t)b * a.nq + qt) * 2 * a.nk;
+  const int nsteps = count;  // one 64-key stage per list entry
+  auto step_kb = [&](int s) { return (ld_const(list, s) >> 2) * kStepK; };
   const int tr_row = tr_row_of(lane);
   const int tr_col = tr_col_of(lane);
   const int* kid_row = a.kid + (size_t)b * a.tk_pad;
@@ -517,8 +516,8 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   // masks and max; both blocks share one shift decision; the first block's
   // P V then runs under the second block's exponentials.
   auto compute = [&](int step, const char* stage) {
-    const int entry = ld_const(list, step >> 1);
-    const int kb = (entry >> 2) * kTile + (step & 1) * kStepK;
+    const int entry = ld_const(list, step);
+    const int kb = (entry >> 2) * kStepK;
     const bool partial = (entry & 3) == 1;
     const char* kt = stage;
     const char* vt = stage + kTileBytes;

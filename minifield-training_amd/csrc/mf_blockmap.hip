@@ -128,15 +128,17 @@ __global__ __launch_bounds__(64) void tile_runs_kernel(MapArgs a) {
   if (lane == 0) *reinterpret_cast<int*>(rec) = n_start;
 }
 
-// Class of tile pair (qi, kj) of row b: 0 EMPTY, 1 PARTIAL, 2 FULL, from the
-// two tiles' run lists (a pair is non-empty iff some query run and key run
-// share an id, with the key run starting at or before the query run's last
-// token when causal; FULL iff both tiles are one run of the same id and the
-// pair lies below the causal diagonal).
-__device__ __forceinline__ int pair_class(const MapArgs& a, int b, int qi, int kj) {
+// Class of the query rows [q_lo, q_hi) of tile qi against the keys [k_lo,
+// k_hi) of tile kj (row b): 0 EMPTY, 1 PARTIAL, 2 FULL, from the two tiles'
+// run lists clipped to the ranges (a pair is non-empty iff some query run and
+// key run share an id, with the key run starting at or before the query
+// run's last token when causal; FULL iff both ranges are one run of the same
+// id and, when causal, every key precedes every query).
+__device__ __forceinline__ int range_class(const MapArgs& a, int b, int qi, int q_lo, int q_hi,
+                                           int kj, int k_lo, int k_hi) {
   const int nq = a.lay.nq, nk = a.lay.nk;
   const bool causal = a.mode == 0;
-  if (causal && kj > qi) return 0;
+  if (causal && k_lo > q_hi - 1) return 0;
   const size_t rec_bytes = sizeof(int) + sizeof(Run) * kMaxRuns;
   const char* base = a.plan + a.lay.runs + rec_bytes * ((size_t)b * (nq + nk));
   const char* rq_rec = base + rec_bytes * qi;
@@ -146,34 +148,65 @@ __device__ __forceinline__ int pair_class(const MapArgs& a, int b, int qi, int k
   const Run* rq = reinterpret_cast<const Run*>(rq_rec + sizeof(int));
   const Run* rk = reinterpret_cast<const Run*>(rk_rec + sizeof(int));
   bool any = false;
+  int q_runs = 0, k_runs = 0, q_id = 0, k_id = 0;
+  bool q_whole = false, k_whole = false;
   for (int x = 0; x < nrq && !any; ++x) {
     const Run u = rq[x];
+    const int us = max(u.start, q_lo), ue = min(u.stop, q_hi);
+    if (us >= ue) continue;
     for (int y = 0; y < nrk; ++y) {
       const Run w = rk[y];
-      if (u.id == w.id && (!causal || w.start <= u.stop - 1)) {
+      const int ws = max(w.start, k_lo), we = min(w.stop, k_hi);
+      if (ws >= we) continue;
+      if (u.id == w.id && (!causal || ws <= ue - 1)) {
         any = true;
         break;
       }
     }
   }
   if (!any) return 0;
-  if (nrq == 1 && nrk == 1 && rq[0].id == rk[0].id && rq[0].start == qi * kTile &&
-      rq[0].stop == (qi + 1) * kTile && rk[0].start == kj * kTile &&
-      rk[0].stop == (kj + 1) * kTile && (!causal || kj < qi))
+  for (int x = 0; x < nrq; ++x) {
+    const int us = max(rq[x].start, q_lo), ue = min(rq[x].stop, q_hi);
+    if (us >= ue) continue;
+    ++q_runs;
+    q_id = rq[x].id;
+    q_whole = us == q_lo && ue == q_hi;
+  }
+  for (int y = 0; y < nrk; ++y) {
+    const int ws = max(rk[y].start, k_lo), we = min(rk[y].stop, k_hi);
+    if (ws >= we) continue;
+    ++k_runs;
+    k_id = rk[y].id;
+    k_whole = ws == k_lo && we == k_hi;
+  }
+  if (q_runs == 1 && k_runs == 1 && q_whole && k_whole && q_id == k_id &&
+      (!causal || k_hi - 1 <= q_lo))
     return 2;
   return 1;
 }
 
-// One block per query-tile row (tile map row and work list of k tiles) or
-// key-tile column (work list of q tiles): the row's or column's pairs are
-// classified one per thread, and the non-empty ones are compacted in
-// increasing tile order as `tile * 4 + class` (ballots within each wave, a
-// prefix over the block's waves through LDS).  Column blocks classify their
-// pairs again rather than waiting for the row blocks' map.
-constexpr int kListThreads = 256;
+// One block per query-tile row (tile map row and work list of 64-key
+// stages) or key-tile column (work list of 64-query stages): the row's or
+// column's stage pairs are classified one per thread, and the non-empty ones
+// are compacted in increasing stage order as `stage * 4 + class` (ballots
+// within each wave, a prefix over the block's waves through LDS).  A tile's
+// class in the tile map is that of its two stages together (EMPTY when both
+// are, FULL when both are).  Column blocks classify their pairs again rather
+// than waiting for the row blocks.  The block has one thread per stage of
+// the longer side, up to kListMaxThreads, so that a row takes one round of
+// classification wherever it fits (a round's latency is that of the run
+// record loads, which no other block hides when the batch is small).
+constexpr int kListMaxThreads = 1024;
 
-__global__ __launch_bounds__(kListThreads) void tile_lists_kernel(MapArgs a) {
-  __shared__ int wave_n[kListThreads / 64];
+static int list_threads(int nq, int nk) {
+  const int stages = 2 * (nq > nk ? nq : nk);
+  const int t = (stages + 63) / 64 * 64;
+  return t < kListMaxThreads ? t : kListMaxThreads;
+}
+
+__global__ __launch_bounds__(kListMaxThreads) void tile_lists_kernel(MapArgs a) {
+  __shared__ int wave_n[kListMaxThreads / 64];
+  const int nwaves = blockDim.x >> 6;
   const int b = blockIdx.y;
   const int t = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -181,26 +214,38 @@ __global__ __launch_bounds__(kListThreads) void tile_lists_kernel(MapArgs a) {
   uint8_t* tmap = reinterpret_cast<uint8_t*>(a.plan + a.lay.tmap) + (size_t)b * nq * nk;
   const bool row = t < nq;
   const int fixed = row ? t : t - nq;
-  const int len = row ? nk : nq;
-  int* list = row ? plan_i32(a.plan, a.lay.qlist) + ((size_t)b * nq + fixed) * nk
-                  : plan_i32(a.plan, a.lay.klist) + ((size_t)b * nk + fixed) * nq;
+  const int len = 2 * (row ? nk : nq);  // stages of the other side
+  int* list = row ? plan_i32(a.plan, a.lay.qlist) + ((size_t)b * nq + fixed) * 2 * nk
+                  : plan_i32(a.plan, a.lay.klist) + ((size_t)b * nk + fixed) * 2 * nq;
   int* count = row ? plan_i32(a.plan, a.lay.qcnt) + (size_t)b * nq + fixed
                    : plan_i32(a.plan, a.lay.kcnt) + (size_t)b * nk + fixed;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   int n = 0;  // entries written by earlier rounds (same value in every thread)
-  for (int base = 0; base < len; base += kListThreads) {
+  for (int base = 0; base < len; base += blockDim.x) {
     const int i = base + threadIdx.x;
     int cls = 0;
     if (i < len) {
-      cls = row ? pair_class(a, b, fixed, i) : pair_class(a, b, i, fixed);
-      if (row) tmap[(size_t)fixed * nk + i] = (uint8_t)cls;
+      const int other = i >> 1, h = i & 1;
+      if (row) {
+        const int q0 = fixed * kTile, k0 = other * kTile + h * (kTile / 2);
+        cls = range_class(a, b, fixed, q0, q0 + kTile, other, k0, k0 + kTile / 2);
+      } else {
+        const int k0 = fixed * kTile, q0 = other * kTile + h * (kTile / 2);
+        cls = range_class(a, b, other, q0, q0 + kTile / 2, fixed, k0, k0 + kTile);
+      }
+    }
+    if (row) {
+      // the tile class from the two stage classes (lanes 2j, 2j + 1)
+      const int pair = __shfl_xor(cls, 1);
+      if (i < len && (i & 1) == 0)
+        tmap[(size_t)fixed * nk + (i >> 1)] =
+            (uint8_t)((cls == 0 && pair == 0) ? 0 : (cls == 2 && pair == 2) ? 2 : 1);
     }
     const uint64_t bits = __ballot(cls != 0);
     if (lane == 0) wave_n[wave] = __popcll(bits);
     __syncthreads();
     int before = 0, total = 0;
-#pragma unroll
-    for (int w = 0; w < kListThreads / 64; ++w) {
+    for (int w = 0; w < nwaves; ++w) {
       before += w < wave ? wave_n[w] : 0;
       total += wave_n[w];
     }
@@ -298,8 +343,8 @@ __global__ __launch_bounds__(256) void placement_ids_kernel(MapArgs a, const int
 
 static void launch_map_tail(const MapArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(tile_runs_kernel, dim3(a.lay.nq + a.lay.nk, a.batch), dim3(64), 0, stream, a);
-  hipLaunchKernelGGL(tile_lists_kernel, dim3(a.lay.nq + a.lay.nk, a.batch), dim3(kListThreads), 0,
-                     stream, a);
+  hipLaunchKernelGGL(tile_lists_kernel, dim3(a.lay.nq + a.lay.nk, a.batch),
+                     dim3(list_threads(a.lay.nq, a.lay.nk)), 0, stream, a);
   hipLaunchKernelGGL(order_kernel, dim3(2), dim3(kOrderThreads), 0, stream, a);
 }
 

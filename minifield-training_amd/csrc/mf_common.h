@@ -189,9 +189,10 @@ __host__ __device__ inline PlanLayout plan_layout(int batch, int q_len, int kv_l
   p.kid = off;   off = align256(off + sizeof(int) * (size_t)batch * p.tk_pad);
   p.tmap = off;  off = align256(off + (size_t)batch * p.nq * p.nk);
   p.qcnt = off;  off = align256(off + sizeof(int) * (size_t)batch * p.nq);
-  p.qlist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nq * p.nk);
+  // work lists of 64-row stages: [B][nq][2 nk] key stages, [B][nk][2 nq] query stages
+  p.qlist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nq * 2 * p.nk);
   p.kcnt = off;  off = align256(off + sizeof(int) * (size_t)batch * p.nk);
-  p.klist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nk * p.nq);
+  p.klist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nk * 2 * p.nq);
   // launch orders: (row, tile) items by decreasing work-list length
   p.qorder = off; off = align256(off + sizeof(int) * (size_t)batch * p.nq);
   p.korder = off; off = align256(off + sizeof(int) * (size_t)batch * p.nk);

@@ -30,18 +30,21 @@ def _check(mode, mask, seg, t, s, device):
     np.testing.assert_array_equal(tm, tm_ref)
     b, nq, nk = tm.shape
     qcnt = plan.section(3, torch.int32, (b, nq)).cpu().numpy()
-    qlist = plan.section(4, torch.int32, (b, nq, nk)).cpu().numpy()
+    qlist = plan.section(4, torch.int32, (b, nq, 2 * nk)).cpu().numpy()
     kcnt = plan.section(5, torch.int32, (b, nk)).cpu().numpy()
-    klist = plan.section(6, torch.int32, (b, nk, nq)).cpu().numpy()
+    klist = plan.section(6, torch.int32, (b, nk, 2 * nq)).cpu().numpy()
+    # work lists hold 64-row stages: query tiles x 64-key stages, 64-query stages x key tiles
+    sq = masks.tile_map(mode, mask, seg, 128, 64, query_length=t)
+    sk = masks.tile_map(mode, mask, seg, 64, 128, query_length=t)
     for r in range(b):
         for qi in range(nq):
-            nz = np.flatnonzero(tm[r, qi])
+            nz = np.flatnonzero(sq[r, qi])
             assert qcnt[r, qi] == nz.size
-            np.testing.assert_array_equal(qlist[r, qi, : nz.size], nz * 4 + tm[r, qi, nz])
+            np.testing.assert_array_equal(qlist[r, qi, : nz.size], nz * 4 + sq[r, qi, nz])
         for kj in range(nk):
-            nz = np.flatnonzero(tm[r, :, kj])
+            nz = np.flatnonzero(sk[r, :, kj])
             assert kcnt[r, kj] == nz.size
-            np.testing.assert_array_equal(klist[r, kj, : nz.size], nz * 4 + tm[r, nz, kj])
+            np.testing.assert_array_equal(klist[r, kj, : nz.size], nz * 4 + sk[r, nz, kj])
     # launch orders: items by decreasing list length (lengths >= 63 tie), stable
     for sec, cnt in ((7, qcnt), (8, kcnt)):
         order = plan.section(sec, torch.int32, (cnt.size,)).cpu().numpy()
@@ -136,8 +139,8 @@ def test_placements_build_the_same_plan(mode, device):
                                (8, torch.int32, (rows * nk,))):
             assert torch.equal(plan.section(sec, dt, shape), ref.section(sec, dt, shape)), sec
         cnt = ref.section(3, torch.int32, (rows, nq)).cpu().numpy()
-        a, r = plan.section(4, torch.int32, (rows, nq, nk)).cpu().numpy(), \
-            ref.section(4, torch.int32, (rows, nq, nk)).cpu().numpy()
+        a, r = plan.section(4, torch.int32, (rows, nq, 2 * nk)).cpu().numpy(), \
+            ref.section(4, torch.int32, (rows, nq, 2 * nk)).cpu().numpy()
         for row in range(rows):
             for qi in range(nq):
                 np.testing.assert_array_equal(a[row, qi, : cnt[row, qi]], r[row, qi, : cnt[row, qi]])
