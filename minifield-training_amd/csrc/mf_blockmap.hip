@@ -128,58 +128,88 @@ __global__ __launch_bounds__(64) void tile_runs_kernel(MapArgs a) {
   if (lane == 0) *reinterpret_cast<int*>(rec) = n_start;
 }
 
-// Class of the query rows [q_lo, q_hi) of tile qi against the keys [k_lo,
-// k_hi) of tile kj (row b): 0 EMPTY, 1 PARTIAL, 2 FULL, from the two tiles'
-// run lists clipped to the ranges (a pair is non-empty iff some query run and
-// key run share an id, with the key run starting at or before the query
-// run's last token when causal; FULL iff both ranges are one run of the same
-// id and, when causal, every key precedes every query).
-__device__ __forceinline__ int range_class(const MapArgs& a, int b, int qi, int q_lo, int q_hi,
-                                           int kj, int k_lo, int k_hi) {
-  const int nq = a.lay.nq, nk = a.lay.nk;
-  const bool causal = a.mode == 0;
-  if (causal && k_lo > q_hi - 1) return 0;
+// A tile's run record with its first kCachedRuns runs loaded into
+// registers: the loads of the count and of those runs are independent, so
+// they take one memory round trip, and the classification below runs from
+// registers unless a record has more runs (then it reads the rest from
+// memory).  Slots past the count are read but never used.
+constexpr int kCachedRuns = 4;
+
+struct RunList {
+  int n;
+  Run r[kCachedRuns];
+  const Run* all;
+};
+
+__device__ __forceinline__ const char* run_record(const MapArgs& a, int b, int t) {
   const size_t rec_bytes = sizeof(int) + sizeof(Run) * kMaxRuns;
-  const char* base = a.plan + a.lay.runs + rec_bytes * ((size_t)b * (nq + nk));
-  const char* rq_rec = base + rec_bytes * qi;
-  const char* rk_rec = base + rec_bytes * (nq + kj);
-  const int nrq = *reinterpret_cast<const int*>(rq_rec);
-  const int nrk = *reinterpret_cast<const int*>(rk_rec);
-  const Run* rq = reinterpret_cast<const Run*>(rq_rec + sizeof(int));
-  const Run* rk = reinterpret_cast<const Run*>(rk_rec + sizeof(int));
-  bool any = false;
-  int q_runs = 0, k_runs = 0, q_id = 0, k_id = 0;
-  bool q_whole = false, k_whole = false;
-  for (int x = 0; x < nrq && !any; ++x) {
-    const Run u = rq[x];
-    const int us = max(u.start, q_lo), ue = min(u.stop, q_hi);
-    if (us >= ue) continue;
-    for (int y = 0; y < nrk; ++y) {
-      const Run w = rk[y];
-      const int ws = max(w.start, k_lo), we = min(w.stop, k_hi);
-      if (ws >= we) continue;
-      if (u.id == w.id && (!causal || ws <= ue - 1)) {
-        any = true;
-        break;
-      }
+  return a.plan + a.lay.runs + rec_bytes * ((size_t)b * (a.lay.nq + a.lay.nk) + (size_t)t);
+}
+
+__device__ __forceinline__ RunList load_runs(const char* rec) {
+  RunList l;
+  l.n = *reinterpret_cast<const int*>(rec);
+  l.all = reinterpret_cast<const Run*>(rec + sizeof(int));
+#pragma unroll
+  for (int i = 0; i < kCachedRuns; ++i) l.r[i] = l.all[i];  // records hold kMaxRuns slots
+  return l;
+}
+
+// The runs of a list clipped to [lo, hi): how many there are, the id of the
+// last one, and whether it covers the whole range.
+struct Clip {
+  int n, id;
+  bool whole;
+};
+
+__device__ __forceinline__ Clip clip_runs(const RunList& l, int lo, int hi) {
+  Clip c = {0, 0, false};
+  auto take = [&](const Run u) {
+    const int s = max(u.start, lo), e = min(u.stop, hi);
+    if (s < e) {
+      ++c.n;
+      c.id = u.id;
+      c.whole = s == lo && e == hi;
     }
+  };
+  if (l.n <= kCachedRuns) {
+#pragma unroll
+    for (int x = 0; x < kCachedRuns; ++x)
+      if (x < l.n) take(l.r[x]);
+  } else {
+    for (int x = 0; x < l.n; ++x) take(l.all[x]);
+  }
+  return c;
+}
+
+// Class of the query rows [q_lo, q_hi) against the keys [k_lo, k_hi) of one
+// row, from the query tile's and the key tile's run lists: 0 EMPTY, 1
+// PARTIAL, 2 FULL.  The pair is non-empty iff some query run and key run,
+// clipped to the ranges, share an id, with the key run starting at or before
+// the query run's last token when causal; FULL iff both ranges are one run of
+// the same id and, when causal, every key precedes every query.
+__device__ __forceinline__ int range_class(bool causal, const RunList& rq, int q_lo, int q_hi,
+                                           const RunList& rk, int k_lo, int k_hi) {
+  if (causal && k_lo > q_hi - 1) return 0;
+  auto meets = [&](const Run u, const Run w) {
+    const int us = max(u.start, q_lo), ue = min(u.stop, q_hi);
+    const int ws = max(w.start, k_lo), we = min(w.stop, k_hi);
+    return us < ue && ws < we && u.id == w.id && (!causal || ws <= ue - 1);
+  };
+  bool any = false;
+  if (rq.n <= kCachedRuns && rk.n <= kCachedRuns) {
+#pragma unroll
+    for (int x = 0; x < kCachedRuns; ++x)
+#pragma unroll
+      for (int y = 0; y < kCachedRuns; ++y)
+        any |= x < rq.n && y < rk.n && meets(rq.r[x], rk.r[y]);
+  } else {
+    for (int x = 0; x < rq.n && !any; ++x)
+      for (int y = 0; y < rk.n && !any; ++y) any = meets(rq.all[x], rk.all[y]);
   }
   if (!any) return 0;
-  for (int x = 0; x < nrq; ++x) {
-    const int us = max(rq[x].start, q_lo), ue = min(rq[x].stop, q_hi);
-    if (us >= ue) continue;
-    ++q_runs;
-    q_id = rq[x].id;
-    q_whole = us == q_lo && ue == q_hi;
-  }
-  for (int y = 0; y < nrk; ++y) {
-    const int ws = max(rk[y].start, k_lo), we = min(rk[y].stop, k_hi);
-    if (ws >= we) continue;
-    ++k_runs;
-    k_id = rk[y].id;
-    k_whole = ws == k_lo && we == k_hi;
-  }
-  if (q_runs == 1 && k_runs == 1 && q_whole && k_whole && q_id == k_id &&
+  const Clip cq = clip_runs(rq, q_lo, q_hi), ck = clip_runs(rk, k_lo, k_hi);
+  if (cq.n == 1 && ck.n == 1 && cq.whole && ck.whole && cq.id == ck.id &&
       (!causal || k_hi - 1 <= q_lo))
     return 2;
   return 1;
@@ -220,18 +250,22 @@ __global__ __launch_bounds__(kListMaxThreads) void tile_lists_kernel(MapArgs a) 
   int* count = row ? plan_i32(a.plan, a.lay.qcnt) + (size_t)b * nq + fixed
                    : plan_i32(a.plan, a.lay.kcnt) + (size_t)b * nk + fixed;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const bool causal = a.mode == 0;
+  // the row's (column's) own tile record, the same for every thread
+  const RunList mine = load_runs(run_record(a, b, row ? fixed : nq + fixed));
   int n = 0;  // entries written by earlier rounds (same value in every thread)
   for (int base = 0; base < len; base += blockDim.x) {
     const int i = base + threadIdx.x;
     int cls = 0;
     if (i < len) {
       const int other = i >> 1, h = i & 1;
+      const RunList theirs = load_runs(run_record(a, b, row ? nq + other : other));
       if (row) {
         const int q0 = fixed * kTile, k0 = other * kTile + h * (kTile / 2);
-        cls = range_class(a, b, fixed, q0, q0 + kTile, other, k0, k0 + kTile / 2);
+        cls = range_class(causal, mine, q0, q0 + kTile, theirs, k0, k0 + kTile / 2);
       } else {
         const int k0 = fixed * kTile, q0 = other * kTile + h * (kTile / 2);
-        cls = range_class(a, b, other, q0, q0 + kTile / 2, fixed, k0, k0 + kTile);
+        cls = range_class(causal, theirs, q0, q0 + kTile / 2, mine, k0, k0 + kTile);
       }
     }
     if (row) {
