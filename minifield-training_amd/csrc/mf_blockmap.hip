@@ -305,8 +305,10 @@ __device__ __forceinline__ int order_bucket(int len) {
 }
 
 __global__ __launch_bounds__(kOrderThreads) void order_kernel(MapArgs a) {
-  // column t of hist belongs to thread t: counts, then scatter cursors
-  __shared__ int hist[kOrderBuckets][kOrderThreads];
+  // column t of hist belongs to thread t: counts, then scatter cursors.  Rows
+  // are padded by one word, so the scan below (lane t walking half of a row)
+  // spreads a wave's reads over the banks instead of one bank.
+  __shared__ int hist[kOrderBuckets][kOrderThreads + 1];
   __shared__ int part[kOrderThreads];
   const bool qside = blockIdx.x == 0;
   const int n = a.batch * (qside ? a.lay.nq : a.lay.nk);
@@ -318,13 +320,14 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(MapArgs a) {
   for (int k = 0; k < kOrderBuckets; ++k) hist[k][t] = 0;
   for (int i = lo; i < hi; ++i) hist[order_bucket(len[i])][t] += 1;
   __syncthreads();
-  // exclusive scan of hist in (bucket, thread) order; thread j owns the
-  // kOrderBuckets consecutive entries starting at flat index j * kOrderBuckets
-  static_assert(kOrderBuckets * kOrderThreads % kOrderThreads == 0, "scan split");
-  int* flat = &hist[0][0];
-  constexpr int E = kOrderBuckets;
+  // exclusive scan of hist in (bucket, thread) order; thread j owns the E
+  // consecutive entries hist[j / 2][(j % 2) E + e], e < E, half of a bucket's
+  // row
+  static_assert(kOrderThreads == 2 * kOrderBuckets, "scan split");
+  constexpr int E = kOrderThreads / 2;
+  int* row = &hist[t >> 1][(t & 1) * E];
   int sum = 0;
-  for (int e = 0; e < E; ++e) sum += flat[t * E + e];
+  for (int e = 0; e < E; ++e) sum += row[e];
   part[t] = sum;
   __syncthreads();
   for (int step = 1; step < kOrderThreads; step <<= 1) {
@@ -335,8 +338,8 @@ __global__ __launch_bounds__(kOrderThreads) void order_kernel(MapArgs a) {
   }
   int base = part[t] - sum;
   for (int e = 0; e < E; ++e) {
-    const int v = flat[t * E + e];
-    flat[t * E + e] = base;
+    const int v = row[e];
+    row[e] = base;
     base += v;
   }
   __syncthreads();
