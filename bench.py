@@ -312,7 +312,39 @@ def rows_leg(steps: int, profile: bool = False):
         p(q), p(k), p(qg), p(kg), p(pos), p(dqo), p(dko), _lib.DTYPE_BF16, b, t, w.q_heads,
         w.kv_heads, w.head_dim, 1e-5, 1e6, p(dqi), p(dki), p(dgq), p(dgk), p(rws), rws_bytes,
         stream)), 3 * (q.nbytes + k.nbytes) + pos.nbytes)
-    del q, k, qo, ko, dqo, dko, dqi, dki, rws
+    del dqo, dko, dqi, dki, rws
+    # the prologue feeding the attention forward (C2, bidirectional): q and k
+    # normalised and rotated, then the forward; against the key half alone
+    # plus the forward with the query half in its query loads (the cos/sin
+    # table launch included)
+    v = torch.randn_like(k)
+    mode = _lib.MODE_PACKED_CAUSAL if w.causal else _lib.MODE_PACKED_BIDIR
+    mask = torch.tensor(w.attention_mask, device=dev)
+    aplan = ops.block_map(seg, mask, mode, t, t)
+    out, lse = torch.empty_like(q), torch.empty(b, w.q_heads, t, device=dev, dtype=torch.float32)
+    table_bytes = L.mf_rope_table_bytes(b, t)
+    table = torch.empty(table_bytes, dtype=torch.uint8, device=dev)
+    scale = w.head_dim ** -0.5
+
+    def separate():
+        _lib.check(L.mf_qk_norm_rope(p(q), p(k), p(qg), p(kg), p(pos), _lib.DTYPE_BF16, b, t,
+                                     w.q_heads, w.kv_heads, w.head_dim, 1e-5, 1e6, p(qo), p(ko),
+                                     stream))
+        _lib.check(L.mf_attn_fwd(p(qo), p(ko), p(v), _lib.DTYPE_BF16, b, t, t, w.q_heads,
+                                 w.kv_heads, w.head_dim, mode, scale, p(aplan.buf), aplan.nbytes,
+                                 p(out), p(lse), stream))
+
+    def fused():
+        _lib.check(L.mf_qk_norm_rope(None, p(k), None, p(kg), p(pos), _lib.DTYPE_BF16, b, t, 0,
+                                     w.kv_heads, w.head_dim, 1e-5, 1e6, None, p(ko), stream))
+        _lib.check(L.mf_attn_fwd_rope_q(p(q), p(ko), p(v), p(qg), p(pos), _lib.DTYPE_BF16, b, t,
+                                        t, w.q_heads, w.kv_heads, w.head_dim, mode, scale, 1e-5,
+                                        1e6, p(aplan.buf), aplan.nbytes, p(table), table_bytes,
+                                        p(out), p(lse), stream))
+
+    run("prologue_then_fwd", separate, 0, "composite")
+    run("fwd_with_query_prologue", fused, 0, "composite")
+    del q, k, qo, ko, v, out, lse, table, aplan
     ch, taps = 1024, 3
     x = [torch.randn(b, t, ch, generator=g, device=dev).to(bf) for _ in range(3)]
     wt = (0.5 * torch.randn(ch, taps, generator=g, device=dev)).to(bf)
@@ -439,14 +471,18 @@ TRAFFIC_KERNELS = {
     # --profile-step launches for two different calls)
     "block_map": (("mf::token_ids_kernel", "mf::tile_runs_kernel", "mf::tile_lists_kernel",
                    "mf::order_kernel"), "C2", None),
-    "attn_fwd": (("mf::attn_fwd_bf16_kernel<",), "C2", None),
+    # the plain forward only (the instances with the query prologue are <., true>)
+    "attn_fwd": (("mf::attn_fwd_bf16_kernel<2, false>", "mf::attn_fwd_bf16_kernel<1, false>"),
+                 "C2", None),
     "attn_bwd_dq": (("mf::bwd_dq_bf16_kernel<",), "C2", None),  # computes D itself in the product call
     "attn_bwd_dkdv": (("mf::bwd_dkdv_bf16_kernel<",), "C2", None),
     "decode": (("mf::decode_prep_kernel", "mf::decode_rows_kernel<", "mf::decode_bf16_kernel<",
                 "mf::decode_combine_kernel<"), "C4", 0),
     "decode_append": (("mf::decode_rows_kernel<", "mf::decode_bf16_kernel<",
                        "mf::decode_combine_kernel<"), "C4", 1),
-    "qk_norm_rope": (("mf::qk_norm_rope_kernel<",), "C2", None),
+    # the first dispatch: the qk_norm_rope row (the composite rows after it launch it again,
+    # the last one for the keys alone)
+    "qk_norm_rope": (("mf::qk_norm_rope_kernel<",), "C2", 0),
     "qk_norm_rope_bwd": (("mf::qk_norm_rope_bwd_kernel<", "mf::rope_gain_reduce_kernel"), "C2",
                          None),
     "segmented_conv": (("mf::segmented_conv_kernel<",), "C2", None),

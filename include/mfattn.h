@@ -187,12 +187,37 @@ int mf_decode_append(const void* q, const void* k_new, const void* v_new,
  * apply_rotary calls of layers/attention.py:62-97 (kernels/normalization.py:7-22,
  * kernels/rotary.py:7-39) on the packed path, where positions restart at
  * every segment (layers/attention.py:224-227).  q_out / k_out may alias q /
- * k.  Layout [B, T, H, 64]; eps and rope_theta as the reference's. */
+ * k.  Layout [B, T, H, 64]; eps and rope_theta as the reference's.  With
+ * q_heads = 0 and q, q_gain, q_out null only the key half runs (the key
+ * operand of mf_attn_fwd_rope_q). */
 int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain,
                     const void* k_gain, const int32_t* positions, int dtype,
                     int batch, int seq_len, int q_heads, int kv_heads,
                     int head_dim, float eps, float rope_theta, void* q_out,
                     void* k_out, void* stream);
+
+/* Packed attention forward (mf_attn_fwd) with the query half of
+ * mf_qk_norm_rope fused into the kernel's query loads, for callers that
+ * need no gradient (prefill, evaluation).  Replaces the composition
+ * rms_norm + apply_rotary of q (kernels/normalization.py:7-22,
+ * kernels/rotary.py:7-39, as layers/attention.py:62-97 applies them) feeding
+ * packed_causal_attention / bidirectional.attention (layers/attention.py:
+ * 224-243): q_raw is the query projection [B, T, Hq, 64] before RMS norm
+ * and RoPE, q_gain its per-dimension gain in the tensor dtype, positions
+ * [B, T] or null as for mf_qk_norm_rope, and k the key after
+ * mf_qk_norm_rope (its tiles reach the kernel by DMA, which cannot transform
+ * them).  out and lse equal those of mf_qk_norm_rope followed by
+ * mf_attn_fwd bit for bit.  bf16 only.  `table` (16-byte aligned,
+ * mf_rope_table_bytes(batch, q_len)) receives each token's bf16 cos/sin
+ * (a first launch), which the attention launch reads. */
+size_t mf_rope_table_bytes(int batch, int q_len);
+int mf_attn_fwd_rope_q(const void* q_raw, const void* k, const void* v,
+                       const void* q_gain, const int32_t* positions, int dtype,
+                       int batch, int q_len, int kv_len, int q_heads,
+                       int kv_heads, int head_dim, int mode, float scale,
+                       float eps, float rope_theta, const void* plan,
+                       size_t plan_bytes, void* table, size_t table_bytes,
+                       void* out, float* lse, void* stream);
 
 /* Backward of mf_qk_norm_rope (the VJP JAX autodiff derives for the
  * reference's rms_norm + apply_rotary, kernels/normalization.py:7-22,

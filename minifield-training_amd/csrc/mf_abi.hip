@@ -16,6 +16,12 @@ hipError_t launch_block_map(const int32_t* seg, const void* mask, int mask_u8, i
 hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32, int batch, int T,
                            int S, int Hq, int Hkv, int mode, float scale, const void* plan,
                            void* out, float* lse, hipStream_t stream);
+hipError_t launch_attn_fwd_rope_q(const void* q_raw, const void* k, const void* v,
+                                  const void* q_gain, const int32_t* positions, int batch, int T,
+                                  int S, int Hq, int Hkv, int mode, float scale, float eps,
+                                  float theta, const void* plan, void* table, void* out,
+                                  float* lse, hipStream_t stream);
+size_t rope_table_bytes(int B, int T);
 hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const void* out,
                            const void* dout, const float* lse, bool f32, int batch, int T, int S,
                            int Hq, int Hkv, int mode, float scale, const void* plan, void* dq,
@@ -351,14 +357,46 @@ int mf_qk_norm_rope(const void* q, const void* k, const void* q_gain, const void
                     const int32_t* positions, int dtype, int batch, int seq_len, int q_heads,
                     int kv_heads, int head_dim, float eps, float rope_theta, void* q_out,
                     void* k_out, void* stream) {
-  if (int rc = check_rope(dtype, batch, seq_len, q_heads, kv_heads, head_dim, rope_theta))
+  // q_heads == 0 with null q, q_gain and q_out: the key half only
+  const bool keys_only = q_heads == 0 && !q && !q_gain && !q_out;
+  if (int rc = check_rope(dtype, batch, seq_len, keys_only ? 1 : q_heads, kv_heads, head_dim,
+                          rope_theta))
     return rc;
-  if (!q || !k || !q_gain || !k_gain || !q_out || !k_out)
+  if ((!keys_only && (!q || !q_gain || !q_out)) || !k || !k_gain || !k_out)
     return fail(MF_ERR_INVALID_ARGUMENT, "a required tensor pointer is null");
   return check_hip(mf::launch_qk_norm_rope(q, k, q_gain, k_gain, positions, dtype == MF_DTYPE_F32,
                                            batch, seq_len, q_heads, kv_heads, eps, rope_theta,
                                            q_out, k_out, static_cast<hipStream_t>(stream)),
                    "mf_qk_norm_rope launch");
+}
+
+size_t mf_rope_table_bytes(int batch, int q_len) {
+  if (batch < 1 || q_len < 1) return 0;
+  return mf::rope_table_bytes(batch, q_len);
+}
+
+int mf_attn_fwd_rope_q(const void* q_raw, const void* k, const void* v, const void* q_gain,
+                       const int32_t* positions, int dtype, int batch, int q_len, int kv_len,
+                       int q_heads, int kv_heads, int head_dim, int mode, float scale, float eps,
+                       float rope_theta, const void* plan, size_t plan_bytes, void* table,
+                       size_t table_bytes, void* out, float* lse, void* stream) {
+  if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
+    return rc;
+  if (int rc = check_rope(dtype, batch, q_len, q_heads, kv_heads, head_dim, rope_theta)) return rc;
+  if (dtype != MF_DTYPE_BF16)
+    return fail(MF_ERR_DTYPE, "mf_attn_fwd_rope_q serves bf16 tensors (dtype code %d)", dtype);
+  if (!q_raw || !k || !v || !q_gain || !plan || !table || !out || !lse)
+    return fail(MF_ERR_INVALID_ARGUMENT, "q_raw, k, v, q_gain, plan, table, out and lse must be non-null");
+  const size_t need = mf_rope_table_bytes(batch, q_len);
+  if (table_bytes < need)
+    return fail(MF_ERR_WORKSPACE, "table holds %zu bytes, %zu needed", table_bytes, need);
+  if (reinterpret_cast<uintptr_t>(table) % 16)
+    return fail(MF_ERR_INVALID_ARGUMENT, "table must be 16-byte aligned");
+  return check_hip(mf::launch_attn_fwd_rope_q(q_raw, k, v, q_gain, positions, batch, q_len, kv_len,
+                                              q_heads, kv_heads, mode, scale, eps, rope_theta,
+                                              plan, table, out, lse,
+                                              static_cast<hipStream_t>(stream)),
+                   "mf_attn_fwd_rope_q launch");
 }
 
 size_t mf_qk_norm_rope_bwd_workspace_bytes(int batch, int seq_len) {

@@ -37,6 +37,12 @@ struct FwdArgs {
   int nq, nk, tq_pad, tk_pad;
   int causal;
   float scale, scale_log2;
+  // query prologue fused into the bf16 kernel's query loads (ROPE instances)
+  const void* q_gain;           // [64], tensor dtype
+  const int32_t* positions;     // [B, T] or null (0 .. T-1 on every row)
+  const uint32_t* rope_table;   // [B * T][32] (bf16 cos | bf16 sin << 16)
+  float eps;
+  float freq[kD / 2];
 };
 
 constexpr int kStepK = 64;          // keys per inner step
@@ -385,7 +391,87 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
 // row sum is unchanged.  Row sums are v_dot2 of the bf16 probabilities with
 // (1, 1), a full-rate VALU op that halves the adds.
 // ---------------------------------------------------------------------------
-template <int HPW>
+// The query half of the attention prologue on the query fragments a lane
+// holds (dims 16 ks + 8 half .. +7 of one query row, ks = 0..3; the other
+// half of the row is in lane ^ 32): RMS normalisation with the per-dimension
+// gain, then the rotary embedding, with the arithmetic and the bf16 rounding
+// points of qk_norm_rope_kernel step for step, so the fragments equal that
+// kernel's output bit for bit.  Its sum of squares adds the fma-chain sums
+// of the eight 8-dim chunks as ((c0 + c1) + (c2 + c3)) + ((c7 + c6) + (c5 +
+// c4)) (its 8-lane DPP butterfly); here chunk 2 ks + half is this lane's and
+// chunk 2 ks + (1 - half) comes from lane ^ 32.  The rotation partner of
+// dims 16 ks + .. (ks < 2) is the same lane's fragment ks + 2.  cos and sin
+// come from the token's row of the table rope_table_kernel fills.
+__device__ __forceinline__ void rope_query(const FwdArgs& a, int b, int qpos, int half,
+                                           bf16x8 (&qf)[4]) {
+  const int t = min(qpos, a.T - 1);
+  // angle pairs of this lane's dims: angles 8 half + i (fragments 0, 2) and
+  // 16 + 8 half + i (fragments 1, 3), i < 8
+  uint32_t cs[2][8];
+  const uint32_t* row = a.rope_table + ((size_t)b * a.T + t) * (kD / 2) + 8 * half;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(row + 16 * j);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(row + 16 * j + 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t l = lo[i], h = hi[i];  // through scalars (vector element reads)
+      cs[j][i] = l;
+      cs[j][4 + i] = h;
+    }
+  }
+  bf16x8 w[4];  // gains of this lane's dims
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    w[ks] = ld_bf16x8(reinterpret_cast<const bf16*>(a.q_gain) + 16 * ks + 8 * half);
+  // chunk sums: mine[ks] is chunk 2 ks + half, theirs[ks] chunk 2 ks + 1 - half
+  float mine[4], theirs[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = (float)qf[ks][i];
+      ss = fmaf(x, x, ss);
+    }
+    mine[ks] = ss;
+    theirs[ks] = __shfl_xor(ss, 32);
+  }
+  float c[8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    c[2 * ks] = half ? theirs[ks] : mine[ks];
+    c[2 * ks + 1] = half ? mine[ks] : theirs[ks];
+  }
+  const float total = ((c[0] + c[1]) + (c[2] + c[3])) + ((c[7] + c[6]) + (c[5] + c[4]));
+  const float inv = rsqrtf(total * (1.f / kD) + a.eps);
+  // n = bf16(bf16(x * inv) * gain), kept as bf16 pairs
+  uint32_t n[4][4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const uint32_t y = round_bf16_pair((float)qf[ks][i] * inv, (float)qf[ks][i + 1] * inv);
+      n[ks][i / 2] = round_bf16_pair(bf16_lo(y) * (float)w[ks][i], bf16_hi(y) * (float)w[ks][i + 1]);
+    }
+  auto nval = [&](int ks, int i) { return (i & 1) ? bf16_hi(n[ks][i / 2]) : bf16_lo(n[ks][i / 2]); };
+  const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int j = ks & 1;  // angle block of fragment ks
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      // rotate_half: dims < 32 take -n[d + 32], dims >= 32 take n[d - 32]
+      const float r = ks < 2 ? -nval(ks + 2, i) : nval(ks - 2, i);
+      const float cv = bf16_lo(cs[j][i]), sv = bf16_hi(cs[j][i]);
+      const uint32_t pq = round_bf16_pair(nval(ks, i) * cv, r * sv);
+      qf[ks][i] = (bf16)__builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pq), ones, 0.f,
+                                                        false);
+    }
+  }
+}
+
+template <int HPW, bool ROPE>
 __global__ __launch_bounds__(256 * HPW) __attribute__((amdgpu_waves_per_eu(2 * HPW)))
 void attn_fwd_bf16_kernel(FwdArgs a) {
   constexpr int W = 4 * HPW;
@@ -416,6 +502,7 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) qf[ks] = ld_bf16x8(src + ks * 16);
   }
+  if constexpr (ROPE) rope_query(a, b, qpos, half, qf);
   drain_memory();
 
   f32x16 oacc[2] = {zero16(), zero16()};
@@ -660,10 +747,80 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
       hipLaunchKernelGGL((attn_fwd_kernel<1, true>), grid, dim3(256), 0, stream, a);
   } else {
     if (hpw == 2)
-      hipLaunchKernelGGL((attn_fwd_bf16_kernel<2>), grid, dim3(512), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_bf16_kernel<2, false>), grid, dim3(512), 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_fwd_bf16_kernel<1>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_bf16_kernel<1, false>), grid, dim3(256), 0, stream, a);
   }
+  return hipGetLastError();
+}
+
+// cos and sin of each token's 32 angles f32(position) * freq[i], rounded to
+// bf16 and packed (cos in the low half): the values qk_norm_rope_kernel
+// computes for the token (the same position, the same sincosf of the same
+// single-precision product) and rounds before use.
+__global__ __launch_bounds__(256) void rope_table_kernel(FwdArgs a, uint32_t* table, size_t n) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= n * (kD / 2)) return;
+  const size_t tok = idx / (kD / 2);
+  const int i = (int)(idx % (kD / 2));
+  const float pos = (float)(a.positions ? a.positions[tok] : (int)(tok % a.T));
+  float f = a.freq[0];
+#pragma unroll
+  for (int j = 1; j < kD / 2; ++j) f = i == j ? a.freq[j] : f;  // no per-lane argument indexing
+  float sv, cv;
+  sincosf(pos * f, &sv, &cv);
+  table[idx] = round_bf16_pair(cv, sv);
+}
+
+size_t rope_table_bytes(int B, int T) { return sizeof(uint32_t) * (kD / 2) * (size_t)B * T; }
+
+hipError_t launch_attn_fwd_rope_q(const void* q_raw, const void* k, const void* v,
+                                  const void* q_gain, const int32_t* positions, int batch, int T,
+                                  int S, int Hq, int Hkv, int mode, float scale, float eps,
+                                  float theta, const void* plan, void* table, void* out,
+                                  float* lse, hipStream_t stream) {
+  FwdArgs a;
+  const PlanLayout lay = plan_layout(batch, T, S);
+  const char* p = reinterpret_cast<const char*>(plan);
+  a.q = q_raw;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.lse = lse;
+  a.qid = reinterpret_cast<const int*>(p + lay.qid);
+  a.kid = reinterpret_cast<const int*>(p + lay.kid);
+  a.qcnt = reinterpret_cast<const int*>(p + lay.qcnt);
+  a.qlist = reinterpret_cast<const int*>(p + lay.qlist);
+  a.qorder = reinterpret_cast<const int*>(p + lay.qorder);
+  a.T = T;
+  a.S = S;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.G = Hq / Hkv;
+  const int hpw = (a.G % 2 == 0) ? 2 : 1;
+  a.hchunks = a.G / hpw;
+  a.nq = lay.nq;
+  a.nk = lay.nk;
+  a.tq_pad = lay.tq_pad;
+  a.tk_pad = lay.tk_pad;
+  a.causal = mode == 0;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.q_gain = q_gain;
+  a.positions = positions;
+  a.rope_table = reinterpret_cast<const uint32_t*>(table);
+  a.eps = eps;
+  // theta ** (-arange(0, D, 2) / D) in single precision (rotary.py:33-35), as
+  // the prologue's launcher computes them
+  for (int i = 0; i < kD / 2; ++i) a.freq[i] = powf(theta, -((float)(2 * i) / (float)kD));
+  const size_t tokens = (size_t)batch * T;
+  hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((tokens * (kD / 2) + 255) / 256)),
+                     dim3(256), 0, stream, a, reinterpret_cast<uint32_t*>(table), tokens);
+  const dim3 grid(Hkv * a.hchunks * batch * lay.nq);
+  if (hpw == 2)
+    hipLaunchKernelGGL((attn_fwd_bf16_kernel<2, true>), grid, dim3(512), 0, stream, a);
+  else
+    hipLaunchKernelGGL((attn_fwd_bf16_kernel<1, true>), grid, dim3(256), 0, stream, a);
   return hipGetLastError();
 }
 

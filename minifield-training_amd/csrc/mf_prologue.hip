@@ -156,7 +156,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
   token_angles(a.positions, tok, a.T, a.freq, lane, cs_l[wave], sn_l[wave]);
   __syncthreads();
   if (token >= total) return;
-  norm_rope_rows<F32>(a.q, a.q_out, a.q_gain, a.Hq, tok, lane, cs_l[wave], sn_l[wave], a.eps);
+  if (a.Hq > 0)  // Hq == 0: the key half only (no query operands)
+    norm_rope_rows<F32>(a.q, a.q_out, a.q_gain, a.Hq, tok, lane, cs_l[wave], sn_l[wave], a.eps);
   norm_rope_rows<F32>(a.k, a.k_out, a.k_gain, a.Hkv, tok, lane, cs_l[wave], sn_l[wave], a.eps);
 }
 

@@ -44,6 +44,8 @@ EXPORTS = (
     "mf_block_map",
     "mf_block_map_placements",
     "mf_attn_fwd",
+    "mf_rope_table_bytes",
+    "mf_attn_fwd_rope_q",
     "mf_attn_bwd_workspace_bytes",
     "mf_attn_bwd",
     "mf_attn_bwd_delta",
@@ -98,6 +100,11 @@ def _load() -> ctypes.CDLL:
     lib.mf_attn_fwd.argtypes = [vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32, f32, vp, sz,
                                 vp, vp, vp]
     lib.mf_attn_fwd.restype = i32
+    lib.mf_rope_table_bytes.argtypes = [i32, i32]
+    lib.mf_rope_table_bytes.restype = sz
+    lib.mf_attn_fwd_rope_q.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,
+                                       f32, f32, f32, vp, sz, vp, sz, vp, vp, vp]
+    lib.mf_attn_fwd_rope_q.restype = i32
     lib.mf_attn_bwd_workspace_bytes.argtypes = [i32, i32, i32]
     lib.mf_attn_bwd_workspace_bytes.restype = sz
     lib.mf_attn_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, i32, i32,

@@ -13,6 +13,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
+from .. import ops
 from ..ops import _ptr, _stream, dtype_code, require_device
 
 
@@ -106,6 +107,24 @@ def qk_norm_rope(query: torch.Tensor, key: torch.Tensor, query_gain: torch.Tenso
     return QKNormRope.apply(q, k, qg, kg, pos, float(eps), float(rope_theta))
 
 
+def key_norm_rope(key: torch.Tensor, key_gain: torch.Tensor, positions=None, *, eps: float,
+                  rope_theta: float) -> torch.Tensor:
+    """The key half of :func:`qk_norm_rope` alone (``mf_qk_norm_rope`` with no query heads):
+    the key operand of :func:`packed_attention_normed_query`.  Forward only."""
+    if torch.is_grad_enabled() and (key.requires_grad or key_gain.requires_grad):
+        raise ValueError("key_norm_rope has no backward; call qk_norm_rope to record gradients")
+    device = require_device(key)
+    b, t, hkv, d = key.shape
+    pos = _positions(positions, b, t, device)
+    k = key.contiguous()
+    kg = key_gain.to(device=device, dtype=key.dtype).contiguous()
+    k_out = torch.empty_like(k)
+    _lib.check(_lib.LIB.mf_qk_norm_rope(None, _ptr(k), None, _ptr(kg), _ptr(pos), dtype_code(k), b,
+                                        t, 0, hkv, d, float(eps), float(rope_theta), None,
+                                        _ptr(k_out), _stream(device)))
+    return k_out
+
+
 def segment_positions(segment_ids: torch.Tensor) -> torch.Tensor:
     """Offset of every token in its run of equal nonzero ids; 0 on padding."""
     device = require_device(segment_ids)
@@ -113,4 +132,38 @@ def segment_positions(segment_ids: torch.Tensor) -> torch.Tensor:
     b, t = seg.shape
     out = torch.empty_like(seg)
     _lib.check(_lib.LIB.mf_segment_positions(_ptr(seg), b, t, _ptr(out), _stream(device)))
+    return out
+
+
+def packed_attention_normed_query(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                  query_gain: torch.Tensor, attention_mask: torch.Tensor,
+                                  segment_ids: torch.Tensor | None, positions=None, *,
+                                  eps: float, rope_theta: float, causal: bool = True,
+                                  plan=None) -> torch.Tensor:
+    """Packed attention of the RMS-normalised, rotated query, the query's norm and RoPE applied
+    in the attention kernel's query loads (``mf_attn_fwd_rope_q``).
+
+    Equal bit for bit to ``qk_norm_rope`` of the query followed by the packed attention
+    (``packed_causal_attention`` when ``causal``, else ``bidirectional.attention`` with segment
+    ids): the composition ``layers/attention.py:214-243`` runs, without the normalised query
+    ever reaching memory.  ``key`` must already be normalised and rotated (``qk_norm_rope``'s
+    key output), ``query`` is the query projection; ``causal=False`` without segment ids is the
+    key-mask mode of ``bidirectional.attention``.  bfloat16, head_dim 64, forward only: inputs
+    that record gradients raise (training calls ``qk_norm_rope`` and the attention).
+    """
+    if torch.is_grad_enabled() and any(
+            x.requires_grad for x in (query, key, value, query_gain)):
+        raise ValueError("packed_attention_normed_query has no backward; call qk_norm_rope and "
+                         "the packed attention to record gradients")
+    device = require_device(query, key, value, attention_mask)
+    b, t, _, d = query.shape
+    mode = (_lib.MODE_PACKED_CAUSAL if causal else
+            _lib.MODE_PACKED_BIDIR if segment_ids is not None else _lib.MODE_KEYMASK_BIDIR)
+    if plan is None:
+        plan = ops.PLANS.get(segment_ids, attention_mask, mode, t, key.shape[1], b)
+    q, k, v = query.contiguous(), key.contiguous(), value.contiguous()
+    qg = query_gain.to(device=device, dtype=query.dtype)
+    pos = _positions(positions, b, t, device)
+    out, _ = ops.attn_fwd_rope_q(q, k, v, qg, pos, plan, mode, d ** -0.5, eps=eps,
+                                 rope_theta=rope_theta)
     return out

@@ -188,6 +188,38 @@ def attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan: Plan, mode
     return out, lse
 
 
+def attn_fwd_rope_q(q_raw: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    q_gain: torch.Tensor, positions: torch.Tensor | None, plan: Plan, mode: int,
+                    scale: float, *, eps: float, rope_theta: float
+                    ) -> tuple[torch.Tensor, torch.Tensor]:
+    """``attn_fwd`` of the query after RMS norm and RoPE, both applied in the kernel's query
+    loads (``mf_attn_fwd_rope_q``): equal bit for bit to ``attn_fwd(qk_norm_rope(q_raw)[0],
+    k, v, ...)`` with ``k`` already normalised and rotated.  bf16; no autograd.
+
+    ``q_gain`` ``[D]`` in the tensor dtype, ``positions`` ``[B, T]`` int32 or ``None``.
+    """
+    code = check_attention_operands(q_raw, k, v, plan, mode)
+    device = require_device(q_raw, k, v, q_gain)
+    if q_raw.dtype != torch.bfloat16:
+        raise ValueError("the fused query prologue serves bfloat16 tensors")
+    b, t, hq, d = q_raw.shape
+    s, hkv = k.shape[1], k.shape[2]
+    if q_gain.shape != (d,) or q_gain.dtype != q_raw.dtype:
+        raise ValueError("q_gain must be a [D] tensor of the query's dtype")
+    if positions is not None and (positions.shape != (b, t) or positions.dtype != torch.int32):
+        raise ValueError("positions must be a [B, T] int32 tensor")
+    q_gain = q_gain.contiguous()
+    table_bytes = _lib.LIB.mf_rope_table_bytes(b, t)
+    table = torch.empty(table_bytes // 4, dtype=torch.int32, device=device)
+    out = torch.empty_like(q_raw)
+    lse = torch.empty((b, hq, t), dtype=torch.float32, device=device)
+    _lib.check(_lib.LIB.mf_attn_fwd_rope_q(
+        _ptr(q_raw), _ptr(k), _ptr(v), _ptr(q_gain), _ptr(positions), code, b, t,
+        s, hq, hkv, d, mode, float(scale), float(eps), float(rope_theta), _ptr(plan.buf),
+        plan.nbytes, _ptr(table), table_bytes, _ptr(out), _ptr(lse), _stream(device)))
+    return out, lse
+
+
 def attn_bwd(q, k, v, out, dout, lse, plan: Plan, mode: int, scale: float):
     check_attention_operands(q, k, v, plan, mode)
     code = same_dtype("query, key, value, output and its gradient", q, k, v, out, dout)

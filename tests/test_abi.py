@@ -112,6 +112,35 @@ def test_decode_append_rejects_bad_arguments():
     assert L.mf_decode_append(*full) == _lib.ERR_HEADS
 
 
+def test_fused_query_prologue_rejects_bad_arguments():
+    L = _lib.LIB
+    buf = ctypes.create_string_buffer(64)  # non-null host addresses: checks fail before launch
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    mis = ctypes.c_void_p(p.value + 4)
+
+    def call(dtype=_lib.DTYPE_BF16, theta=10000.0, ptr=p, table=p, table_bytes=1 << 20, d=64):
+        return L.mf_attn_fwd_rope_q(ptr, p, p, p, None, dtype, 2, 8, 8, 4, 2, d, 0, 0.125,
+                                    1e-6, theta, p, 1 << 30, table, table_bytes, p, p, None)
+
+    assert L.mf_rope_table_bytes(2, 8) == 2 * 8 * 32 * 4
+    assert L.mf_rope_table_bytes(0, 8) == 0
+    assert call(dtype=_lib.DTYPE_F32) == _lib.ERR_DTYPE
+    assert "bf16" in _msg()
+    assert call(theta=0.0) == _lib.ERR_INVALID_ARGUMENT
+    assert "rope_theta" in _msg()
+    assert call(d=128) == _lib.ERR_HEAD_DIM
+    assert call(ptr=None) == _lib.ERR_INVALID_ARGUMENT
+    assert call(table_bytes=16) == _lib.ERR_WORKSPACE
+    assert "table holds 16 bytes" in _msg()
+    assert call(table=mis) == _lib.ERR_INVALID_ARGUMENT
+    assert "16-byte aligned" in _msg()
+    # the key-only prologue: q_heads = 0 needs q, q_gain and q_out null
+    assert L.mf_qk_norm_rope(p, None, None, p, None, _lib.DTYPE_BF16, 2, 8, 0, 2, 64, 1e-6,
+                             1e4, None, p, None) == _lib.ERR_INVALID_ARGUMENT
+    assert L.mf_qk_norm_rope(None, None, None, p, None, _lib.DTYPE_BF16, 2, 8, 0, 2, 64, 1e-6,
+                             1e4, None, p, None) == _lib.ERR_INVALID_ARGUMENT  # k null
+
+
 def test_error_codes_map_to_value_errors():
     rc = _fwd(hq=3)
     with pytest.raises(ValueError, match="divisible"):

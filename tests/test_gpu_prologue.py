@@ -173,3 +173,70 @@ def test_segment_positions_ragged_and_repeated_ids(device):
         seg = np.repeat(rng.integers(0, 4, size=(3, length // 7 + 1)), 7, axis=1)[:, :length]
         got = prologue.segment_positions(torch.tensor(seg.astype(np.int32), device=device))
         np.testing.assert_array_equal(got.cpu().numpy(), oprol.segment_positions(seg))
+
+
+@pytest.mark.parametrize("name, hq, hkv, mode, pos_kind", [
+    ("C1", 16, 8, 0, "segment"),
+    ("C1", 8, 8, 1, "none"),      # G = 1: one head per workgroup
+    ("C1", 12, 4, 0, "large"),    # G = 3; positions far beyond T (sincosf's long reduction)
+    ("C1", 16, 2, 2, "none"),     # key-mask mode, G = 8
+    ("C2", 16, 8, 1, "segment"),  # the bench shape
+    ("C5", 16, 8, 0, "segment"),
+])
+def test_fused_query_prologue_equals_prologue_then_attention(name, hq, hkv, mode, pos_kind, device):
+    """mf_attn_fwd_rope_q (norm and RoPE of q in the attention kernel's query loads) against
+    mf_qk_norm_rope followed by mf_attn_fwd: output and lse bit for bit."""
+    from mfattn import ops
+    w = packing.make_workload(name)
+    b, t, d = w.batch, w.length, 64
+    say("fused query prologue", name, hq, hkv, mode, pos_kind)
+    g = torch.Generator(device=device).manual_seed(w.seed)
+    mk = lambda h, s: (torch.randn(b, t, h, d, generator=g, device=device) * s).bfloat16()
+    q_raw, k_raw, v = mk(hq, 3.0), mk(hkv, 3.0), mk(hkv, 1.0)
+    qg = (1 + 0.2 * torch.randn(d, generator=g, device=device)).bfloat16()
+    kg = (1 + 0.2 * torch.randn(d, generator=g, device=device)).bfloat16()
+    if pos_kind == "segment":
+        pos = torch.tensor(oprol.segment_positions(w.segment_ids), device=device)
+    elif pos_kind == "large":
+        pos = torch.randint(0, 1 << 24, (b, t), generator=g, device=device, dtype=torch.int32)
+    else:
+        pos = None
+    eps, theta, scale = 1e-5, 10000.0, d ** -0.5
+    qn, kn = prologue.qk_norm_rope(q_raw, k_raw, qg, kg, pos, eps=eps, rope_theta=theta)
+    mask = torch.tensor(w.attention_mask, device=device)
+    seg = None if mode == 2 else torch.tensor(w.segment_ids, device=device)
+    plan = ops.block_map(seg, mask, mode, t, t)
+    ref_out, ref_lse = ops.attn_fwd(qn, kn, v, plan, mode, scale)
+    out, lse = ops.attn_fwd_rope_q(q_raw, kn, v, qg, pos, plan, mode, scale, eps=eps,
+                                   rope_theta=theta)
+    torch.cuda.synchronize()
+    same_out = (out.view(torch.int16) == ref_out.view(torch.int16)).float().mean().item()
+    say(f"  out bit-equal fraction {same_out:.6f}")
+    assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+    assert torch.equal(lse, ref_lse)
+
+
+def test_fused_query_prologue_at_the_layer_level(device):
+    """The kernels-level entry equals qk_norm_rope + packed_causal_attention, and refuses
+    inputs that record gradients."""
+    from mfattn.kernels import attention
+    w = packing.make_workload("C1")
+    b, t, hq, hkv, d = w.batch, w.length, 8, 4, 64
+    g = torch.Generator(device=device).manual_seed(7)
+    mk = lambda h: (torch.randn(b, t, h, d, generator=g, device=device) * 2).bfloat16()
+    q_raw, k_raw, v = mk(hq), mk(hkv), mk(hkv)
+    qg, kg = torch.rand(d, generator=g, device=device) + 0.5, torch.rand(d, generator=g, device=device) + 0.5
+    mask = torch.tensor(w.attention_mask, device=device)
+    seg = torch.tensor(w.segment_ids, device=device)
+    pos = prologue.segment_positions(seg)
+    qn, kn = prologue.qk_norm_rope(q_raw, k_raw, qg, kg, pos, eps=1e-6, rope_theta=1e6)
+    ref = attention.packed_causal_attention(qn, kn, v, mask, seg, backend="hip")
+    got = prologue.packed_attention_normed_query(q_raw, kn, v, qg, mask, seg, pos, eps=1e-6,
+                                                 rope_theta=1e6)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    # the key half alone equals the key output of the joint call
+    assert torch.equal(prologue.key_norm_rope(k_raw, kg, pos, eps=1e-6, rope_theta=1e6).view(torch.int16),
+                       kn.view(torch.int16))
+    with pytest.raises(ValueError, match="no backward"):
+        prologue.packed_attention_normed_query(q_raw.requires_grad_(), kn, v, qg, mask, seg, pos,
+                                               eps=1e-6, rope_theta=1e6)
