@@ -3,14 +3,18 @@
 The library is loaded at import.  There is no fallback: if it is missing or
 does not load, importing this module raises ``ImportError`` naming the file
 and the build command, so nothing can silently run another implementation.
+``MFATTN_LIB`` may name another build of the same library (the tests' build
+with the host code under AddressSanitizer and UBSan).
 """
 
 from __future__ import annotations
 
 import ctypes
+import os
 import pathlib
 
-LIB_PATH = pathlib.Path(__file__).resolve().parent / "libmfattn.so"
+LIB_PATH = pathlib.Path(os.environ.get("MFATTN_LIB") or
+                        pathlib.Path(__file__).resolve().parent / "libmfattn.so")
 
 # status codes (include/mfattn.h)
 OK = 0

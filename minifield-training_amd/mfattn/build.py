@@ -74,5 +74,49 @@ def build(verbose: bool = True) -> pathlib.Path:
     return OUT
 
 
+# Host code under AddressSanitizer and UBSan: the C ABI (argument checks,
+# plan layout, workspace sizes) compiled with the sanitizers on its host pass
+# only, linked with the regular kernel objects.  It loads into a process that
+# preloads the sanitizer runtime (``sanitizer_runtime()``); the GPU code is
+# the regular build's.
+SAN_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O1", "-g", "-fno-omit-frame-pointer",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xarch_host", "-fsanitize=address",
+    "-Xarch_host", "-fsanitize=undefined",
+    "-Xarch_host", "-fno-sanitize-recover=undefined",
+]
+SAN_OUT = CSRC / "_build" / "libmfattn_san.so"
+
+
+def sanitizer_runtime() -> pathlib.Path | None:
+    """The clang AddressSanitizer runtime of the ROCm toolchain (it carries UBSan's handlers)."""
+    hits = sorted(pathlib.Path("/opt/rocm/llvm/lib/clang").glob(
+        "*/lib/linux/libclang_rt.asan-x86_64.so"))
+    return hits[-1] if hits else None
+
+
+def build_sanitized() -> pathlib.Path:
+    objdir = CSRC / "_build"
+    if not OUT.exists() or not all((objdir / (s.stem + ".o")).exists()
+                                   for s in CSRC.glob("*.hip")):
+        build(verbose=False)
+    abi = objdir / "mf_abi_san.o"
+    proc = subprocess.run([_hipcc(), *SAN_FLAGS, "-c", str(CSRC / "mf_abi.hip"), "-o", str(abi)],
+                          capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for the sanitizer build:\n{proc.stderr}")
+    objs = [str(o) for o in sorted(objdir.glob("*.o"))
+            if o.name not in ("mf_abi.o", "mf_abi_san.o")]
+    proc = subprocess.run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o",
+                           str(SAN_OUT), str(abi), *objs], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed for the sanitizer build:\n{proc.stderr}")
+    return SAN_OUT
+
+
 if __name__ == "__main__":
     build()
