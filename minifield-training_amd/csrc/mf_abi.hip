@@ -290,9 +290,6 @@ int check_decode_shape(int dtype, int batch, int capacity, int q_heads, int kv_h
   if (head_dim != mf::kD)
     return fail(MF_ERR_SHAPE, "Cached attention query/KV shapes are incompatible");
   if (q_heads % kv_heads) return fail(MF_ERR_HEADS, "Query heads must be divisible by KV heads");
-  if (q_heads / kv_heads > 8)
-    return fail(MF_ERR_HEADS, "Decode serves at most 8 query heads per KV head (got %d)",
-                q_heads / kv_heads);
   return MF_OK;
 }
 

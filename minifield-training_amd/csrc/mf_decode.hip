@@ -193,10 +193,6 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
         st_u32x4(&lds.k[(u >> 3) * kPitch + (u & 7) * 8], kr[i]);
         st_u32x4(&lds.v[(u >> 3) * kPitch + (u & 7) * 8], vr[i]);
       }
-      for (int e = tid; e < a.G * kD; e += 256) {
-        const int g = e / kD, d = e % kD;
-        lds.q[g][d] = (float)reinterpret_cast<const bf16*>(a.q)[((size_t)b * a.Hq + kvh * a.G + g) * kD + d];
-      }
     } else {
       const float* ks = reinterpret_cast<const float*>(a.k);
       const float* vs = reinterpret_cast<const float*>(a.v);
@@ -215,10 +211,17 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
         st_u32x4(&lds.k[(u >> 4) * kPitchF + (u & 15) * 4], kr[i]);
         st_u32x4(&lds.v[(u >> 4) * kPitchF + (u & 15) * 4], vr[i]);
       }
-      for (int e = tid; e < a.G * kD; e += 256) {
-        const int g = e / kD, d = e % kD;
-        lds.q[g][d] = reinterpret_cast<const float*>(a.q)[((size_t)b * a.Hq + kvh * a.G + g) * kD + d];
-      }
+    }
+
+    // The group's query heads in chunks of kMaxG, each against the staged
+    // K and V (any number of query heads per KV head).
+    for (int g0 = 0; g0 < a.G; g0 += kMaxG) {
+    const int gc = min(kMaxG, a.G - g0);
+    for (int e = tid; e < gc * kD; e += 256) {
+      const int g = e / kD, d = e % kD;
+      const size_t qi = ((size_t)b * a.Hq + kvh * a.G + g0 + g) * kD + d;
+      if constexpr (F32) lds.q[g][d] = reinterpret_cast<const float*>(a.q)[qi];
+      else lds.q[g][d] = (float)reinterpret_cast<const bf16*>(a.q)[qi];
     }
     __syncthreads();
 
@@ -236,7 +239,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
             const float kv = (float)kx[e];
 #pragma unroll
             for (int g = 0; g < kMaxG; ++g)
-              if (g < a.G) sc[g] = fmaf(lds.q[g][c8 * 8 + e], kv, sc[g]);
+              if (g < gc) sc[g] = fmaf(lds.q[g][c8 * 8 + e], kv, sc[g]);
           }
         }
       } else {
@@ -247,7 +250,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
           for (int e = 0; e < 4; ++e)
 #pragma unroll
             for (int g = 0; g < kMaxG; ++g)
-              if (g < a.G) sc[g] = fmaf(lds.q[g][c4 * 4 + e], kx[e], sc[g]);
+              if (g < gc) sc[g] = fmaf(lds.q[g][c4 * 4 + e], kx[e], sc[g]);
         }
       }
     }
@@ -255,7 +258,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
     float mx2[kMaxG];
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) {
-      if (g >= a.G) break;
+      if (g >= gc) break;
       const float s2 = tid < n ? sc[g] * c : kNegInf;
       const float wm = wave_max(s2);
       if (lane == 0) lds.red[g][wave] = wm;
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) {
-      if (g >= a.G) break;
+      if (g >= gc) break;
       mx2[g] = fmaxf(fmaxf(lds.red[g][0], lds.red[g][1]), fmaxf(lds.red[g][2], lds.red[g][3]));
       const float p = tid < n ? fast_exp2(fmaf(sc[g], c, -mx2[g])) : 0.f;
       if (tid < C) lds.p[g][tid] = p;
@@ -272,14 +275,14 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
     float lsum[kMaxG];
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) {
-      if (g >= a.G) break;
+      if (g >= gc) break;
       const float ws = wave_sum(tid < C ? lds.p[g][tid] : 0.f);
       lsum[g] = ws;
     }
     __syncthreads();  // everyone has read red[] for the max
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g) {
-      if (g >= a.G) break;
+      if (g >= gc) break;
       if (lane == 0) lds.red[g][wave] = lsum[g];
     }
 
@@ -293,22 +296,24 @@ __global__ __launch_bounds__(256) void decode_kernel(DecArgs a) {
       else vv = lds.v[t * kPitchF + lane];
 #pragma unroll
       for (int g = 0; g < kMaxG; ++g)
-        if (g < a.G) acc[g] = fmaf(lds.p[g][t], vv, acc[g]);
+        if (g < gc) acc[g] = fmaf(lds.p[g][t], vv, acc[g]);
     }
 #pragma unroll
     for (int g = 0; g < kMaxG; ++g)
-      if (g < a.G) lds.acc[wave][g][lane] = acc[g];
+      if (g < gc) lds.acc[wave][g][lane] = acc[g];
     __syncthreads();
     if (wave == 0) {
-      for (int g = 0; g < a.G; ++g) {
+      for (int g = 0; g < gc; ++g) {
         const float o = lds.acc[0][g][lane] + lds.acc[1][g][lane] + lds.acc[2][g][lane] +
                         lds.acc[3][g][lane];
-        const int h = kvh * a.G + g;
+        const int h = kvh * a.G + g0 + g;
         float* dst = a.partial + (((size_t)b * a.Hq + h) * a.maxc + chunk) * (2 + kD);
         dst[2 + lane] = o;
         if (lane == 0) dst[0] = mx2[g];
         if (lane == 1) dst[1] = lds.red[g][0] + lds.red[g][1] + lds.red[g][2] + lds.red[g][3];
       }
+    }
+    __syncthreads();  // q, p, red and acc are rewritten by the next chunk
     }
     __syncthreads();  // LDS reused by the next item
   }

@@ -38,6 +38,9 @@ def test_reference_cached_fixture(device):
     (torch.bfloat16, 4, 2),   # 2
     (torch.bfloat16, 6, 2),   # 3: served by the LDS-staged kernel
     (torch.bfloat16, 16, 2),  # 8
+    (torch.bfloat16, 32, 2),  # 16: the LDS-staged kernel in two passes of 8 heads
+    (torch.float32, 24, 2),   # 12: one pass of 8 heads and one of 4
+    (torch.bfloat16, 40, 1),  # 40: five passes, one KV head
 ])
 def test_ragged_lengths_and_edges(dtype, hq, hkv, device):
     rng = np.random.default_rng(5)
@@ -99,6 +102,7 @@ def test_scalar_length_broadcasts_and_backends_agree(device):
     (torch.bfloat16, 2, 2),   # G = 1
     (torch.bfloat16, 16, 2),  # G = 8
     (torch.bfloat16, 6, 2),   # G = 3: the prep kernel appends, the LDS-staged kernel decodes
+    (torch.bfloat16, 32, 2),  # G = 16: likewise, in two passes of 8 query heads
 ])
 def test_decode_step_appends_per_row(dtype, hq, hkv, device):
     """Ragged KV-cache append + decode (layers/attention.py:309-317, one slot per row).
