@@ -709,10 +709,13 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   }
 }
 
-hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32, int batch,
-                           int T, int S, int Hq, int Hkv, int mode, float scale,
-                           const void* plan, void* out, float* lse, hipStream_t stream) {
-  FwdArgs a;
+// Arguments of one forward launch: operands, the plan's sections, shapes and
+// the workgroup shape (heads per workgroup: 2 when the GQA group splits into
+// pairs, else 1).
+static FwdArgs fwd_args(const void* q, const void* k, const void* v, int batch, int T, int S,
+                        int Hq, int Hkv, int mode, float scale, const void* plan, void* out,
+                        float* lse, int* hpw) {
+  FwdArgs a = {};
   const PlanLayout lay = plan_layout(batch, T, S);
   const char* p = reinterpret_cast<const char*>(plan);
   a.q = q;
@@ -730,8 +733,8 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
   a.Hq = Hq;
   a.Hkv = Hkv;
   a.G = Hq / Hkv;
-  const int hpw = (a.G % 2 == 0) ? 2 : 1;
-  a.hchunks = a.G / hpw;
+  *hpw = (a.G % 2 == 0) ? 2 : 1;
+  a.hchunks = a.G / *hpw;
   a.nq = lay.nq;
   a.nk = lay.nk;
   a.tq_pad = lay.tq_pad;
@@ -739,7 +742,15 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
   a.causal = mode == 0;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
-  const dim3 grid(Hkv * a.hchunks * batch * lay.nq);
+  return a;
+}
+
+hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32, int batch,
+                           int T, int S, int Hq, int Hkv, int mode, float scale,
+                           const void* plan, void* out, float* lse, hipStream_t stream) {
+  int hpw;
+  const FwdArgs a = fwd_args(q, k, v, batch, T, S, Hq, Hkv, mode, scale, plan, out, lse, &hpw);
+  const dim3 grid(Hkv * a.hchunks * batch * a.nq);
   if (f32) {
     if (hpw == 2)
       hipLaunchKernelGGL((attn_fwd_kernel<2, true>), grid, dim3(256), 0, stream, a);
@@ -779,33 +790,8 @@ hipError_t launch_attn_fwd_rope_q(const void* q_raw, const void* k, const void* 
                                   int S, int Hq, int Hkv, int mode, float scale, float eps,
                                   float theta, const void* plan, void* table, void* out,
                                   float* lse, hipStream_t stream) {
-  FwdArgs a;
-  const PlanLayout lay = plan_layout(batch, T, S);
-  const char* p = reinterpret_cast<const char*>(plan);
-  a.q = q_raw;
-  a.k = k;
-  a.v = v;
-  a.out = out;
-  a.lse = lse;
-  a.qid = reinterpret_cast<const int*>(p + lay.qid);
-  a.kid = reinterpret_cast<const int*>(p + lay.kid);
-  a.qcnt = reinterpret_cast<const int*>(p + lay.qcnt);
-  a.qlist = reinterpret_cast<const int*>(p + lay.qlist);
-  a.qorder = reinterpret_cast<const int*>(p + lay.qorder);
-  a.T = T;
-  a.S = S;
-  a.Hq = Hq;
-  a.Hkv = Hkv;
-  a.G = Hq / Hkv;
-  const int hpw = (a.G % 2 == 0) ? 2 : 1;
-  a.hchunks = a.G / hpw;
-  a.nq = lay.nq;
-  a.nk = lay.nk;
-  a.tq_pad = lay.tq_pad;
-  a.tk_pad = lay.tk_pad;
-  a.causal = mode == 0;
-  a.scale = scale;
-  a.scale_log2 = scale * kLog2e;
+  int hpw;
+  FwdArgs a = fwd_args(q_raw, k, v, batch, T, S, Hq, Hkv, mode, scale, plan, out, lse, &hpw);
   a.q_gain = q_gain;
   a.positions = positions;
   a.rope_table = reinterpret_cast<const uint32_t*>(table);
@@ -816,7 +802,7 @@ hipError_t launch_attn_fwd_rope_q(const void* q_raw, const void* k, const void* 
   const size_t tokens = (size_t)batch * T;
   hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((tokens * (kD / 2) + 255) / 256)),
                      dim3(256), 0, stream, a, reinterpret_cast<uint32_t*>(table), tokens);
-  const dim3 grid(Hkv * a.hchunks * batch * lay.nq);
+  const dim3 grid(Hkv * a.hchunks * batch * a.nq);
   if (hpw == 2)
     hipLaunchKernelGGL((attn_fwd_bf16_kernel<2, true>), grid, dim3(512), 0, stream, a);
   else
