@@ -15,8 +15,8 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import (BF16_TOL, DT, check_bf16, max_abs, operands, say, short_segment_rows,
-                      torch_reference)
+from _helpers import (BF16_TOL, DT, check_bf16, check_bf16_sum, max_abs, operands, say,
+                      short_segment_rows, torch_reference)
 from mfattn import _lib, ops
 from mfattn.kernels import attention, bidirectional
 from oracle import attention as oatt
@@ -143,6 +143,83 @@ def test_random_layouts_against_oracle(mode, dtype, t, device):
             np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
         else:
             check_bf16(f"random layout mode {mode} T {t} {name}", a, r)
+
+
+def _rounding_magnitudes(mode, q, k, v, do, mask, seg):
+    """FP64 magnitude sums that bound what bf16 rounding inside the kernels can do to each
+    output: P is rounded before P V and dS before dS K and dS^T Q (relative 2**-9 each), and
+    D = rowsum(dO * O) is formed from the bf16-rounded O; the outputs are rounded once.
+    Returns, per output element, the sum of the magnitudes of the terms those roundings touch
+    (plus the output's own magnitude)."""
+    q, k, v, do = (np.asarray(x, np.float64) for x in (q, k, v, do))
+    b, t, hq, d = q.shape
+    g = hq // k.shape[2]
+    scale = d ** -0.5
+    qid, kid = masks._token_ids(mode, mask, seg, t)
+    causal = mode == masks.MODE_PACKED_CAUSAL
+    m_out, m_dq = np.zeros_like(q), np.zeros_like(q)
+    m_dk, m_dv = np.zeros_like(k), np.zeros_like(v)
+    for row in range(b):
+        for ident in np.unique(qid[row][qid[row] != masks.Q_INACTIVE]):
+            qi, kj = np.flatnonzero(qid[row] == ident), np.flatnonzero(kid[row] == ident)
+            if kj.size == 0:
+                continue
+            allowed = (kj[None, :] <= qi[:, None]) if causal else np.ones((qi.size, kj.size), bool)
+            for h in range(hq):
+                kh = h // g
+                sc = np.where(allowed, q[row, qi, h] @ k[row, kj, kh].T * scale, -np.inf)
+                m = np.where(allowed.any(1), sc.max(1), 0.0)
+                e = np.where(allowed, np.exp(sc - m[:, None]), 0.0)
+                p = e / np.maximum(e.sum(1), 1e-300)[:, None]
+                o = p @ v[row, kj, kh]
+                go = do[row, qi, h]
+                ds = p * (go @ v[row, kj, kh].T - (go * o).sum(1)[:, None])
+                dd = (np.abs(go) * np.abs(o)).sum(1)[:, None]  # bound on D's rounding error / 2**-9
+                m_out[row, qi, h] = p @ np.abs(v[row, kj, kh])
+                m_dv[row, kj, kh] += p.T @ np.abs(go)
+                m_dq[row, qi, h] = scale * ((np.abs(ds) + p * dd) @ np.abs(k[row, kj, kh]))
+                m_dk[row, kj, kh] += scale * ((np.abs(ds) + p * dd).T @ np.abs(q[row, qi, h]))
+    return m_out, m_dq, m_dk, m_dv
+
+
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_large_logits_and_rising_maxima(mode, dtype, device):
+    """Logits with a spread of tens (q, k scaled by 4) and keys scaled up along the sequence, so
+    each query's running maximum keeps rising: the online softmax rescales at every step (its
+    shift moves once the maximum grows by more than 8 in log2 units).  FP64 oracle; fp32 at
+    1e-5, bf16 beyond what rounding P, dS, O and the outputs can move them (these logits make
+    dQ and dK sums of large, cancelling terms, which the absolute bf16 bar cannot hold)."""
+    rng = np.random.default_rng(77 + mode)
+    b, t, hq, hkv = 2, 517, 4, 2
+    say("large logits", mode, dtype)
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, DT[dtype], 4.0)
+    ramp = torch.linspace(0.25, 2.0, t, device=device)[None, :, None, None]
+    k = (k.float() * ramp).to(k.dtype)
+    if mode == 2:
+        mask = (rng.random((b, t)) > 0.2).astype(np.int32)
+        seg = None
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, torch.tensor(mask, device=device))  # noqa: E731
+    else:
+        seg = np.repeat(rng.integers(1, 4, size=(b, t // 150 + 1)), 150, axis=1)[:, :t].astype(np.int32)
+        mask = np.ones((b, t), np.int32)
+        tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+        if mode == 0:
+            fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+        else:
+            fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = oatt.grouped_fp64(mode, *(x.float().cpu().numpy() for x in (q, k, v)), mask, seg,
+                            d_out=do.float().cpu().numpy())
+    mags = None if dtype == "float32" else _rounding_magnitudes(
+        mode, *(x.float().cpu().numpy() for x in (q, k, v, do)), mask, seg)
+    for i, (name, a, r) in enumerate(zip(("out", "dq", "dk", "dv"), got, ref)):
+        assert bool(torch.isfinite(a).all()), name
+        if dtype == "float32":
+            np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5 * max(1.0, np.abs(r).max()),
+                                       err_msg=name)
+        else:
+            check_bf16_sum(f"large logits mode {mode} {name}", a, r, mags[i] + np.abs(r))
 
 
 @pytest.mark.parametrize("hq, hkv", [(4, 4), (8, 2), (6, 2), (3, 1), (16, 2), (2, 2)])
