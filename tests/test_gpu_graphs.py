@@ -1,0 +1,71 @@
+"""The packed attention step under HIP graph capture.
+
+Serving loops and training steps capture their launches once and replay them
+(hipGraph through torch.cuda.CUDAGraph).  Every launch of the step -- the
+block map's kernels, the forward, the backward -- goes to the caller's stream
+with no allocation, memset or host synchronisation inside the library, so the
+captured step replays with new inputs and gives what the eager calls give,
+bit for bit (the kernels are deterministic).  Replays alternate with eager
+work and synchronisations, and every replay is checked.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import say
+from mfattn import ops
+from oracle import packing
+
+pytestmark = pytest.mark.gpu
+
+
+def _step(q, k, v, do, seg, mask, mode):
+    plan = ops.block_map(seg, mask, mode, q.shape[1], k.shape[1])
+    out, lse = ops.attn_fwd(q, k, v, plan, mode, q.shape[-1] ** -0.5)
+    dq, dk, dv = ops.attn_bwd(q, k, v, out, do, lse, plan, mode, q.shape[-1] ** -0.5)
+    return out, lse, dq, dk, dv
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_captured_step_replays_equal_eager(mode, device):
+    rng = np.random.default_rng(11 + mode)
+    b, t, hq, hkv, d = 2, 1000, 8, 4, 64
+    say("graph capture", mode)
+    seg_np = np.zeros((b, t), np.int32)
+    for row in range(b):
+        pos, sid = 0, 1
+        while pos < t:
+            n = int(rng.integers(20, 400))
+            seg_np[row, pos:pos + n] = sid
+            pos, sid = pos + n, sid + 1
+        seg_np[row, t - 37:] = 0  # trailing padding
+    seg = torch.tensor(seg_np, device=device)
+    mask = (seg != 0).to(torch.int32)
+    mk = lambda h: torch.empty(b, t, h, d, device=device, dtype=torch.bfloat16)  # noqa: E731
+    q, k, v, do = mk(hq), mk(hkv), mk(hkv), mk(hq)
+
+    def fill(seed):
+        g = torch.Generator(device=device).manual_seed(seed)
+        for x in (q, k, v, do):
+            x.copy_(torch.randn(x.shape, generator=g, device=device))
+
+    fill(0)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        _step(q, k, v, do, seg, mask, mode)  # warm-up on a side stream, as capture requires
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = _step(q, k, v, do, seg, mask, mode)
+    for trial in range(3):
+        fill(100 + trial)
+        graph.replay()
+        torch.cuda.synchronize(device)
+        eager = _step(q, k, v, do, seg, mask, mode)
+        torch.cuda.synchronize(device)
+        for name, a, r in zip(("out", "lse", "dq", "dk", "dv"), captured, eager):
+            same = torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a.view(torch.int16),
+                               r.view(torch.int32) if r.dtype == torch.float32 else r.view(torch.int16))
+            assert same, (trial, name)
