@@ -81,7 +81,7 @@ size_t mf_plan_bytes(int batch, int q_len, int kv_len);
 /* Block-mask builder.  Replaces the dense validity grids of
  * kernels/attention.py:79-108 (_packed_valid_mask) and
  * kernels/bidirectional.py:21-31 with a per-(row, 128-query tile, 128-key
- * tile) EMPTY/PARTIAL/FULL map plus compacted per-tile work lists.
+ * tile) EMPTY/PARTIAL/FULL map plus compacted work lists of 64-row stages.
  * segment_ids may be NULL only in MF_MODE_KEYMASK_BIDIR; there `mask` is the
  * [B, kv_len] key mask and q_len may differ from kv_len.  In the packed
  * modes q_len must equal kv_len. */
