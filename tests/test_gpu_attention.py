@@ -145,6 +145,43 @@ def test_random_layouts_against_oracle(mode, dtype, t, device):
             check_bf16(f"random layout mode {mode} T {t} {name}", a, r)
 
 
+@pytest.mark.parametrize("t", [1, 2, 63, 64, 65, 127, 128, 129, 191])
+@pytest.mark.parametrize("mode", [0, 1, 2])
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_stage_and_tile_edge_lengths(t, mode, dtype, device):
+    """Lengths on and beside the 64-row stage and 128-token tile edges (the work lists' units),
+    two segments per row meeting at the middle, 16 query heads on one KV head (G = 16) for odd
+    lengths and 4 on 2 otherwise; forward and backward against the FP64 oracle."""
+    rng = np.random.default_rng(1000 + 10 * t + mode)
+    b = 2
+    hq, hkv = (16, 1) if t % 2 else (4, 2)
+    say("edge length", t, mode, dtype, (hq, hkv))
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, DT[dtype], 0.7)
+    if mode == 2:
+        mask = np.ones((b, t), np.int32)
+        mask[1, : (t + 1) // 2] = 0
+        seg = None
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, torch.tensor(mask, device=device))  # noqa: E731
+    else:
+        seg = np.ones((b, t), np.int32)
+        seg[:, t // 2:] = 2
+        seg[1, -1] = 0  # a padding token at the end of row 1
+        mask = (seg != 0).astype(np.int32)
+        tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+        if mode == 0:
+            fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+        else:
+            fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = oatt.grouped_fp64(mode, *(x.float().cpu().numpy() for x in (q, k, v)), mask, seg,
+                            d_out=do.float().cpu().numpy())
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        if dtype == "float32":
+            np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
+        else:
+            check_bf16(f"edge T {t} mode {mode} {name}", a, r)
+
+
 def _rounding_magnitudes(mode, q, k, v, do, mask, seg):
     """FP64 magnitude sums that bound what bf16 rounding inside the kernels can do to each
     output: P is rounded before P V and dS before dS K and dS^T Q (relative 2**-9 each), and
