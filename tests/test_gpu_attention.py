@@ -182,6 +182,43 @@ def test_stage_and_tile_edge_lengths(t, mode, dtype, device):
             check_bf16(f"edge T {t} mode {mode} {name}", a, r)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_randomized_shapes(seed, device):
+    """Seeded random calls: batch 1-3, lengths 1-400 (key lengths of their own in the key-mask
+    mode), GQA ratios 1-4, ids with holes, repeats and negative values, fp32 and bf16, forward
+    and backward against the FP64 oracle."""
+    rng = np.random.default_rng(5000 + seed)
+    mode = int(rng.integers(0, 3))
+    b, t = int(rng.integers(1, 4)), int(rng.integers(1, 401))
+    s = int(rng.integers(1, 401)) if mode == 2 else t
+    hkv = int(rng.integers(1, 4))
+    hq = hkv * int(rng.integers(1, 5))
+    dtype = "float32" if seed % 2 else "bfloat16"
+    say("randomized", seed, mode, dtype, (b, t, s, hq, hkv))
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, DT[dtype], 0.6, s=s)
+    if mode == 2:
+        mask = (rng.random((b, s)) > 0.25).astype(np.int32)
+        seg = None
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, torch.tensor(mask, device=device))  # noqa: E731
+    else:
+        run = int(rng.integers(1, 90))
+        seg = np.repeat(rng.integers(-3, 5, size=(b, t // run + 1)), run, axis=1)[:, :t].astype(np.int32)
+        mask = (rng.random((b, t)) > 0.15).astype(np.int32)
+        tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+        if mode == 0:
+            fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+        else:
+            fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = oatt.grouped_fp64(mode, *(x.float().cpu().numpy() for x in (q, k, v)), mask, seg,
+                            d_out=do.float().cpu().numpy())
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        if dtype == "float32":
+            np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
+        else:
+            check_bf16(f"randomized {seed} {name}", a, r)
+
+
 def _rounding_magnitudes(mode, q, k, v, do, mask, seg):
     """FP64 magnitude sums that bound what bf16 rounding inside the kernels can do to each
     output: P is rounded before P V and dS before dS K and dS^T Q (relative 2**-9 each), and
