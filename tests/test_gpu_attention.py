@@ -15,8 +15,8 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import (BF16_TOL, DT, check_bf16, check_bf16_sum, max_abs, operands, say,
-                      short_segment_rows, torch_reference)
+from _helpers import (BF16_HALF_ULP, BF16_TOL, DT, check_bf16, check_bf16_sum, max_abs,
+                      operands, say, short_segment_rows, torch_reference)
 from mfattn import _lib, ops
 from mfattn.kernels import attention, bidirectional
 from oracle import attention as oatt
@@ -217,6 +217,66 @@ def test_randomized_shapes(seed, device):
             np.testing.assert_allclose(a.cpu().numpy(), r, rtol=1e-5, atol=1e-5, err_msg=name)
         else:
             check_bf16(f"randomized {seed} {name}", a, r)
+
+
+def _chunked_row(rng, t):
+    """One row of ``t`` tokens cut into chunks of 128-token multiples (up to 4096 tokens), each
+    filled with whole segments of 16-128 tokens (one in eight of 129-4096, cut at the chunk's
+    end) and 5 % padding; ids increase along the row, so no segment crosses a chunk edge."""
+    bounds = [0]
+    while bounds[-1] < t:
+        bounds.append(min(t, bounds[-1] + 128 * int(rng.integers(1, 33))))
+    seg = np.zeros(t, np.int32)
+    sid = 0
+    for lo, hi in zip(bounds, bounds[1:]):
+        pos = lo
+        while pos < hi:
+            n = int(rng.integers(16, 129)) if rng.random() < 0.875 else int(rng.integers(129, 4097))
+            n = min(n, hi - pos)
+            if rng.random() >= 0.05:
+                sid += 1
+                seg[pos:pos + n] = sid
+            pos += n
+    return seg[None], bounds
+
+
+def _packed_fn(mode, mask, seg, device):
+    tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+    if mode == 0:
+        return lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+    return lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_long_row_against_reference_and_its_windows(mode, device):
+    """One row of 524,288 tokens (a 1 GiB bf16 query row, 4096 query tiles: the block map
+    classifies each tile's 8192 stages in eight rounds): forward and backward within the bf16
+    bar of the fp32 reference (evaluated on the device in float32), and bit-identical to the
+    same calls on windows of whole chunks cut out of the row at its start, middle and end."""
+    t, hq, hkv = 524288, 16, 8
+    rng = np.random.default_rng(524288 + mode)
+    seg, bounds = _chunked_row(rng, t)
+    mask = (seg != 0).astype(np.int32)
+    say("long row", t, "mode", mode, "chunks", len(bounds) - 1)
+    gen = torch.Generator(device=device).manual_seed(524288 + mode)
+    mk = lambda h, sc: (torch.randn((1, t, h, 64), generator=gen, device=device) * sc).to(torch.bfloat16)  # noqa: E731
+    q, k, v, do = mk(hq, 0.5), mk(hkv, 0.5), mk(hkv, 0.5), mk(hq, 1.0)
+    got = _grads(_packed_fn(mode, mask, seg, device), q, k, v, do)
+    ref = torch_reference(mode, q, k, v, mask, seg, do)
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        diff = (a.float() - r).abs()
+        raw, excess = diff.max().item(), (diff - BF16_HALF_ULP * r.abs()).max().item()
+        say(f"long row mode {mode} {name}: max-abs {raw:.3e} beyond-rounding {excess:.3e}")
+        assert excess < BF16_TOL, (name, raw, excess)
+    del ref, diff
+    n = len(bounds) - 1
+    for i0, i1 in ((0, 3), (n // 2, n // 2 + 3), (n - 3, n)):
+        lo, hi = bounds[i0], bounds[i1]
+        say("window", lo, hi)
+        sub = _grads(_packed_fn(mode, mask[:, lo:hi], seg[:, lo:hi], device),
+                     *(x[:, lo:hi] for x in (q, k, v, do)))
+        for name, a, w in zip(("out", "dq", "dk", "dv"), got, sub):
+            assert torch.equal(a[:, lo:hi], w), (name, lo, hi)
 
 
 def _rounding_magnitudes(mode, q, k, v, do, mask, seg):

@@ -144,3 +144,43 @@ def test_placements_build_the_same_plan(mode, device):
         for row in range(rows):
             for qi in range(nq):
                 np.testing.assert_array_equal(a[row, qi, : cnt[row, qi]], r[row, qi, : cnt[row, qi]])
+
+
+def _long_rows():
+    import sys
+    sys.path.insert(0, str(pathlib.Path(__file__).parent / "golden"))
+    import make_long_rows  # noqa: E402
+
+    gold = json.loads((pathlib.Path(__file__).parent / "golden" / "long_rows.json").read_text())
+    return make_long_rows, gold
+
+
+@pytest.mark.parametrize("name", ["causal_98304", "bidir_131072", "keymask_65600x131149"])
+def test_long_rows_against_oracle_digests(name, device):
+    """Rows of 65,600-131,149 tokens: over 1024 64-row stages per tile, so the work lists are
+    classified in several rounds.  Every plan section is bit-exact with the oracle's, compared
+    through the SHA-256 digests that tests/golden/make_long_rows.py stored; ids directly."""
+    mlr, gold = _long_rows()
+    mode, mask, seg, t, s = mlr.long_row_layout(name)
+    want = gold[name]
+    assert (want["mode"], want["batch"], want["q_len"], want["kv_len"]) == (mode, mask.shape[0], t, s)
+    say("long block map", name, "T", t, "S", s)
+    st = None if seg is None else torch.tensor(seg, device=device)
+    plan = ops.block_map(st, torch.tensor(mask, device=device), mode, t, s)
+    tm = plan.tile_map().cpu().numpy()
+    b, nq, nk = tm.shape
+    qcnt = plan.section(3, torch.int32, (b, nq)).cpu().numpy()
+    kcnt = plan.section(5, torch.int32, (b, nk)).cpu().numpy()
+    got = mlr.digest_sections(
+        tm, qcnt, plan.section(4, torch.int32, (b, nq, 2 * nk)).cpu().numpy(),
+        kcnt, plan.section(6, torch.int32, (b, nk, 2 * nq)).cpu().numpy(),
+        plan.section(7, torch.int32, (b * nq,)).cpu().numpy(),
+        plan.section(8, torch.int32, (b * nk,)).cpu().numpy())
+    assert int(qcnt.sum()) == want["stages"]
+    for key, digest in want["digests"].items():
+        assert got[key] == digest, key
+    qid, kid = masks._token_ids(mode, mask, seg, t)
+    gq = plan.section(0, torch.int32, (b, nq * 128)).cpu().numpy()
+    gk = plan.section(1, torch.int32, (b, nk * 128)).cpu().numpy()
+    np.testing.assert_array_equal(gq[:, :t], np.where(qid != masks.Q_INACTIVE, qid, 0))
+    np.testing.assert_array_equal(gk[:, :s], np.where(kid != masks.K_INACTIVE, kid, 0))
