@@ -452,11 +452,11 @@ def cpu_leg(seconds: float):
 # HBM traffic of the measured kernels (rocprofv3 PMC passes)
 #
 #   cd /tmp && export TMPDIR=/tmp
-#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d <root>/gpurun_out/pmc_fetch -o run \
+#   rocprofv3 --pmc FETCH_SIZE --output-format csv -d <out>/pmc_fetch -o run \
 #       -- python3 <root>/bench.py --profile-step
-#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d <root>/gpurun_out/pmc_write -o run \
+#   rocprofv3 --pmc WRITE_SIZE --output-format csv -d <out>/pmc_write -o run \
 #       -- python3 <root>/bench.py --profile-step
-#   python3 bench.py --traffic gpurun_out/pmc_fetch gpurun_out/pmc_write
+#   python3 bench.py --traffic <out>/pmc_fetch <out>/pmc_write
 #
 # --profile-step runs one device-to-device copy of CALIB_BYTES (the
 # calibration: it reads and writes exactly that many bytes), one C2 step,
