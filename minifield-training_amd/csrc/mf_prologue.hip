@@ -14,12 +14,12 @@
 // off): the normalised value, its product with the gain, cos and sin, the
 // two rotation products and their sum.
 //
-// Layout: one wave per token.  Lanes 0..31 compute the token's 32 angles'
-// cos/sin into LDS; then lane (g = lane / 8, dl = lane % 8) owns dims
+// Layout: one wave per token.  Lane (g = lane / 8, dl = lane % 8) owns dims
 // 8 dl .. 8 dl + 7 of head g of a group of 8 heads, so a 16-byte (bf16) or
 // two 16-byte (fp32) loads per lane move 8 whole head rows, the sum of
 // squares reduces over 8 lanes with DPP, and the rotation partner (dims
-// +- 32) is lane dl ^ 4 of the same head.
+// +- 32) is lane dl ^ 4 of the same head.  Lanes j and j + 32 evaluate the
+// token's angle j; the lanes read their dims' cos/sin by shuffle.
 #include <algorithm>
 #include <type_traits>
 
@@ -47,118 +47,205 @@ __device__ __forceinline__ float dpp_xor_sum8(float x) {
   return x;
 }
 
+// ---------------------------------------------------------------------------
+// Rows as loaded: one 8-head group of a token (16 bytes per lane in bf16, 32
+// in fp32), kept raw until the group is computed, so that every load of a
+// token is in flight before the first use.
+// ---------------------------------------------------------------------------
+template <bool F32> struct RopeRow;
+template <> struct RopeRow<false> { bf16x8 v; };
+template <> struct RopeRow<true> { f32x4 a, b; };
+
 template <bool F32>
-__device__ __forceinline__ void norm_rope_rows(const void* src, void* dst, const void* gain, int H,
-                                               size_t token, int lane, const float* cs,
-                                               const float* sn, float eps) {
+__device__ __forceinline__ RopeRow<F32> load_rope_row(const void* src, size_t base) {
+  RopeRow<F32> r;
+  if constexpr (F32) {
+    const float* p = reinterpret_cast<const float*>(src) + base;
+    r.a = *reinterpret_cast<const f32x4*>(p);
+    r.b = *reinterpret_cast<const f32x4*>(p + 4);
+  } else {
+    r.v = ld_bf16x8(reinterpret_cast<const bf16*>(src) + base);
+  }
+  return r;
+}
+
+template <bool F32>
+__device__ __forceinline__ void rope_row_floats(const RopeRow<F32>& r, float (&x)[8]) {
+  if constexpr (F32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = r.a[i], x[4 + i] = r.b[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = (float)r.v[i];
+  }
+}
+
+// The gains (cast to the tensor dtype) of the lane's 8 dims.
+template <bool F32>
+__device__ __forceinline__ void load_gains(const void* gain, int dl, float (&w)[8]) {
   typedef typename std::conditional<F32, float, bf16>::type T;
-  const int g = lane >> 3, dl = lane & 7;
-  float w[8], c[8], s[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = (float)reinterpret_cast<const T*>(gain)[8 * dl + i];
+}
+
+// The token's position as a float: positions[tok], or its index in the row
+// when there are no positions.
+__device__ __forceinline__ float token_position(const int32_t* positions, size_t tok, int T) {
+  return (float)(positions ? positions[tok] : (int)(tok % T));
+}
+
+// cos and sin of the token's angles for the lane's dims 8 dl .. 8 dl + 7:
+// lanes j and j + 32 evaluate angle j = f32(position) * freq[j] (freq is
+// the lane's freq[lane mod 32]), and each
+// lane reads its dims' angles (d mod 32) by shuffle.  The fused forward's
+// rope table evaluates the same sincosf of the same product.
+template <bool F32>
+__device__ __forceinline__ void token_cos_sin(float pos, float freq, int dl, float (&c)[8],
+                                              float (&s)[8]) {
+  float sv, cv;
+  sincosf(pos * freq, &sv, &cv);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int d = 8 * dl + i;
-    w[i] = (float)reinterpret_cast<const T*>(gain)[d];  // gain cast to the tensor dtype
-    c[i] = cs[d & 31];
-    s[i] = sn[d & 31];
+    c[i] = __shfl(cv, (8 * dl + i) & 31);
+    s[i] = __shfl(sv, (8 * dl + i) & 31);
     if constexpr (!F32) {
       c[i] = round_bf16(c[i]);
       s[i] = round_bf16(s[i]);
     }
   }
-  for (int h0 = 0; h0 < H; h0 += 8) {
-    const int h = h0 + g;
-    const bool live = h < H;
-    const size_t base = (token * H + min(h, H - 1)) * kD + 8 * dl;
-    float x[8];
-    if constexpr (F32) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + base);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(src) + base + 4);
+}
+
+// Norm and rotation of one loaded group: lane (g, dl) holds dims 8 dl ..
+// 8 dl + 7 of head g.  Every lane takes part (the 8-lane sum and the
+// rotation shuffle); only live lanes store.
+template <bool F32>
+__device__ __forceinline__ void norm_rope_store(const RopeRow<F32>& xin, void* dst, size_t base,
+                                                bool live, const float (&w)[8],
+                                                const float (&c)[8], const float (&s)[8], int dl,
+                                                float eps) {
+  float x[8];
+  rope_row_floats<F32>(xin, x);
+  float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i];
-    } else {
-      const bf16x8 a = ld_bf16x8(reinterpret_cast<const bf16*>(src) + base);
+  for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+  const float inv = rsqrtf(dpp_xor_sum8(ss) * (1.f / kD) + eps);
+  float n[8], r[8];
+  if constexpr (F32) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) x[i] = (float)a[i];
+    for (int i = 0; i < 8; ++i) n[i] = x[i] * inv * w[i];
+  } else {
+    // the normalised value, then its product with the gain, each rounded to
+    // bf16; two elements per conversion
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const uint32_t y = round_bf16_pair(x[i] * inv, x[i + 1] * inv);
+      const uint32_t z = round_bf16_pair(bf16_lo(y) * w[i], bf16_hi(y) * w[i + 1]);
+      n[i] = bf16_lo(z);
+      n[i + 1] = bf16_hi(z);
     }
-    float ss = 0.f;
+  }
+  // rotate_half: dims d < 32 take -n[d + 32], dims d >= 32 take n[d - 32]
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
-    const float inv = rsqrtf(dpp_xor_sum8(ss) * (1.f / kD) + eps);
-    float n[8], r[8];
-    if constexpr (F32) {
+  for (int i = 0; i < 8; ++i) {
+    const float o = __shfl_xor(n[i], 4);
+    r[i] = dl < 4 ? -o : o;
+  }
+  if (!live) return;
+  if constexpr (F32) {
+    f32x4 a, b;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) n[i] = x[i] * inv * w[i];
-    } else {
-      // the normalised value, then its product with the gain, each rounded
-      // to bf16; two elements per conversion
-#pragma unroll
-      for (int i = 0; i < 8; i += 2) {
-        const uint32_t y = round_bf16_pair(x[i] * inv, x[i + 1] * inv);
-        const uint32_t z = round_bf16_pair(bf16_lo(y) * w[i], bf16_hi(y) * w[i + 1]);
-        n[i] = bf16_lo(z);
-        n[i + 1] = bf16_hi(z);
-      }
+    for (int i = 0; i < 4; ++i) {
+      a[i] = fmaf(n[i], c[i], r[i] * s[i]);
+      b[i] = fmaf(n[4 + i], c[4 + i], r[4 + i] * s[4 + i]);
     }
-    // rotate_half: dims d < 32 take -n[d + 32], dims d >= 32 take n[d - 32]
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base) = a;
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base + 4) = b;
+  } else {
+    // the two rotation products rounded to bf16 by one conversion and added
+    // by one dot product with (1, 1) (exact products, one fp32 rounding)
+    const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+    bf16x8 o;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float o = __shfl_xor(n[i], 4);
-      r[i] = dl < 4 ? -o : o;
+      const uint32_t pq = round_bf16_pair(n[i] * c[i], r[i] * s[i]);
+      o[i] = (bf16)__builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pq), ones, 0.f, false);
     }
-    if (!live) continue;
-    if constexpr (F32) {
-      f32x4 a, b;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = fmaf(n[i], c[i], r[i] * s[i]);
-        b[i] = fmaf(n[4 + i], c[4 + i], r[4 + i] * s[4 + i]);
-      }
-      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base) = a;
-      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(dst) + base + 4) = b;
-    } else {
-      // the two rotation products rounded to bf16 by one conversion and added
-      // by one dot product with (1, 1) (exact products, one fp32 rounding)
-      const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
-      bf16x8 o;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t pq = round_bf16_pair(n[i] * c[i], r[i] * s[i]);
-        o[i] = (bf16)__builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pq), ones, 0.f, false);
-      }
-      *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(dst) + base) = o;
-    }
+    *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(dst) + base) = o;
   }
 }
 
-// cos and sin of the token's 32 angles f32(position) * freq[i] into LDS
-// (lanes 0..31), shared by the forward and the backward so both use the
-// same values.
-__device__ __forceinline__ void token_angles(const int32_t* positions, size_t tok, int T,
-                                             const float* freq, int lane, float* cs, float* sn) {
-  const int t = (int)(tok % T);
-  const float pos = (float)(positions ? positions[tok] : t);
-  if (lane < kD / 2) {
-    float sv, cv;
-    sincosf(pos * freq[lane], &sv, &cv);
-    cs[lane] = cv;
-    sn[lane] = sv;
-  }
-}
+// 8-head groups of one token (q groups first, then k) loaded per batch
+// before any of them is computed.
+constexpr int kRopeFwdBatch = 4;
 
+// One wave per token, no LDS and no barrier: the token's row loads (all of
+// them when the q and k heads fill at most four groups) are issued first,
+// the angles are evaluated while they are in flight, then each group is
+// normalised, rotated and stored.
 template <bool F32>
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
-  __shared__ float cs_l[4][kD / 2], sn_l[4][kD / 2];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const size_t token = (size_t)blockIdx.x * 4 + wave;  // b * T + t
-  const size_t total = (size_t)a.B * a.T;
-  const size_t tok = token < total ? token : total - 1;  // tail waves redo the last token, no store
-  token_angles(a.positions, tok, a.T, a.freq, lane, cs_l[wave], sn_l[wave]);
-  __syncthreads();
-  if (token >= total) return;
-  if (a.Hq > 0)  // Hq == 0: the key half only (no query operands)
-    norm_rope_rows<F32>(a.q, a.q_out, a.q_gain, a.Hq, tok, lane, cs_l[wave], sn_l[wave], a.eps);
-  norm_rope_rows<F32>(a.k, a.k_out, a.k_gain, a.Hkv, tok, lane, cs_l[wave], sn_l[wave], a.eps);
+  const int g = lane >> 3, dl = lane & 7;
+  const size_t tok = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // b * T + t
+  if (tok >= (size_t)a.B * a.T) return;
+  const int gq = (a.Hq + 7) >> 3;  // Hq == 0: the key half only (no query operands)
+  const int groups = gq + ((a.Hkv + 7) >> 3);
+  auto locate = [&](int i, const void*& src, void*& dst, size_t& base, bool& live) {
+    const bool isq = i < gq;
+    const int H = isq ? a.Hq : a.Hkv;
+    const int h = 8 * (isq ? i : i - gq) + g;
+    live = h < H;
+    base = (tok * H + min(h, H - 1)) * kD + 8 * dl;
+    src = isq ? a.q : a.k;
+    dst = isq ? a.q_out : a.k_out;
+  };
+  // the small operands first (position, the lane's frequency, the gains):
+  // loads complete in issue order, so anything loaded after the rows could
+  // only be read once every row had arrived
+  const float pos = token_position(a.positions, tok, a.T);
+  const float fq = a.freq[lane & 31];
+  const RopeRow<F32> gq_raw = load_rope_row<F32>(gq > 0 ? a.q_gain : a.k_gain, 8 * dl);
+  const RopeRow<F32> gk_raw = load_rope_row<F32>(a.k_gain, 8 * dl);
+  RopeRow<F32> x[kRopeFwdBatch];
+  auto load_batch = [&](int i0) {
+#pragma unroll
+    for (int j = 0; j < kRopeFwdBatch; ++j) {
+      if (i0 + j < groups) {
+        const void* src;
+        void* dst;
+        size_t base;
+        bool live;
+        locate(i0 + j, src, dst, base, live);
+        x[j] = load_rope_row<F32>(src, base);
+      }
+    }
+  };
+  float wq[8], wk[8], c[8], s[8];
+  auto store_batch = [&](int i0) {
+#pragma unroll
+    for (int j = 0; j < kRopeFwdBatch; ++j) {
+      if (i0 + j < groups) {
+        const void* src;
+        void* dst;
+        size_t base;
+        bool live;
+        locate(i0 + j, src, dst, base, live);
+        norm_rope_store<F32>(x[j], dst, base, live, i0 + j < gq ? wq : wk, c, s, dl, a.eps);
+      }
+    }
+  };
+  load_batch(0);
+  // the angles and gains only after the first rows are in flight (they would
+  // otherwise be hoisted above them as loop invariants)
+  __builtin_amdgcn_sched_barrier(0);
+  rope_row_floats<F32>(gq_raw, wq);  // gains cast to the tensor dtype (read in it)
+  rope_row_floats<F32>(gk_raw, wk);
+  token_cos_sin<F32>(pos, fq, dl, c, s);
+  store_batch(0);
+  for (int i0 = kRopeFwdBatch; i0 < groups; i0 += kRopeFwdBatch) {
+    load_batch(i0);
+    store_batch(i0);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -193,37 +280,6 @@ struct RopeBwdArgs {
 
 constexpr int kRopeBwdBlocks = 1024;  // workgroups of the backward (fewer for short inputs)
 constexpr int kRopeBatch = 2;          // (token, head group) rows loaded before any is computed
-
-// One 8-head group of a token's rows as loaded (16 bytes per lane in bf16,
-// 32 in fp32), kept raw until the group is computed, so that every load of
-// a token is in flight before the first use.
-template <bool F32> struct RopeRow;
-template <> struct RopeRow<false> { bf16x8 v; };
-template <> struct RopeRow<true> { f32x4 a, b; };
-
-template <bool F32>
-__device__ __forceinline__ RopeRow<F32> load_rope_row(const void* src, size_t base) {
-  RopeRow<F32> r;
-  if constexpr (F32) {
-    const float* p = reinterpret_cast<const float*>(src) + base;
-    r.a = *reinterpret_cast<const f32x4*>(p);
-    r.b = *reinterpret_cast<const f32x4*>(p + 4);
-  } else {
-    r.v = ld_bf16x8(reinterpret_cast<const bf16*>(src) + base);
-  }
-  return r;
-}
-
-template <bool F32>
-__device__ __forceinline__ void rope_row_floats(const RopeRow<F32>& r, float (&x)[8]) {
-  if constexpr (F32) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = r.a[i], x[4 + i] = r.b[i];
-  } else {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = (float)r.v[i];
-  }
-}
 
 // The VJP of one loaded group: lane (g, dl) holds dims 8 dl .. 8 dl + 7 of
 // head g.  Every lane takes part (shuffles and the 8-lane sums); only live
@@ -291,13 +347,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(RopeBwdArgs a) {
   const size_t stride = (size_t)gridDim.x * 4;
   const int gq = (a.Hq + 7) >> 3;
   const int groups = gq + ((a.Hkv + 7) >> 3);  // 8-head groups of a token, q first
-  typedef typename std::conditional<F32, float, bf16>::type T;
   float wq[8], wk[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    wq[i] = (float)reinterpret_cast<const T*>(a.q_gain)[8 * dl + i];
-    wk[i] = (float)reinterpret_cast<const T*>(a.k_gain)[8 * dl + i];
-  }
+  load_gains<F32>(a.q_gain, dl, wq);
+  load_gains<F32>(a.k_gain, dl, wk);
   float dwq[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dwk[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   // (token, group) of this wave's rows; no barrier inside the loop, so the
   // waves of a block need not run the same number of tokens
@@ -313,6 +365,9 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(RopeBwdArgs a) {
     dst = isq ? a.dq : a.dk;
   };
   for (size_t tok = (size_t)blockIdx.x * 4 + wave; tok < total; tok += stride) {
+    // position and frequency loaded before the rows
+    const float pos = token_position(a.positions, tok, a.T);
+    const float fq = a.freq[lane & 31];
     float c[8], s[8];
     for (int i0 = 0; i0 < groups; i0 += kRopeBatch) {
       RopeRow<F32> x[kRopeBatch], go[kRopeBatch];
@@ -328,22 +383,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope_bwd_kernel(RopeBwdArgs a) {
           go[j] = load_rope_row<F32>(gsrc, base);
         }
       }
-      if (i0 == 0) {
-        // the token's 32 angles (lanes j and j + 32 compute angle j), read
-        // by each lane for its dims with shuffles; overlaps the loads
-        const float pos = (float)(a.positions ? a.positions[tok] : (int)(tok % a.T));
-        float sv, cv;
-        sincosf(pos * a.freq[lane & 31], &sv, &cv);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          c[i] = __shfl(cv, (8 * dl + i) & 31);
-          s[i] = __shfl(sv, (8 * dl + i) & 31);
-          if constexpr (!F32) {
-            c[i] = round_bf16(c[i]);
-            s[i] = round_bf16(s[i]);
-          }
-        }
-      }
+      // the token's angles, evaluated while its loads are in flight
+      if (i0 == 0) token_cos_sin<F32>(pos, fq, dl, c, s);
 #pragma unroll
       for (int j = 0; j < kRopeBatch; ++j) {
         if (i0 + j < groups) {

@@ -30,9 +30,12 @@ FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # min/max need no NaN quieting: masked scores are -inf, never NaN
+    # min/max need no NaN quieting: masked scores are -inf, never NaN.  IEEE
+    # mode stays on (no -mno-amdgpu-ieee): the device libraries are built with
+    # it, and the inliner does not inline across a mode mismatch, which turned
+    # every threadIdx/blockIdx/blockDim read, rsqrtf and sincosf into a call
+    # (a stack frame, and a wait for every load in flight at each call)
     "-fno-honor-nans",
-    "-mno-amdgpu-ieee",
     "-Wall",
     "-Wno-unused-function",
 ]
