@@ -279,7 +279,7 @@ struct RopeBwdArgs {
 };
 
 constexpr int kRopeBwdBlocks = 1024;  // workgroups of the backward (fewer for short inputs)
-constexpr int kRopeBatch = 2;          // (token, head group) rows loaded before any is computed
+constexpr int kRopeBatch = 3;          // (token, head group) rows loaded before any is computed
 
 // The VJP of one loaded group: lane (g, dl) holds dims 8 dl .. 8 dl + 7 of
 // head g.  Every lane takes part (shuffles and the 8-lane sums); only live
