@@ -94,11 +94,11 @@ __device__ __forceinline__ float token_position(const int32_t* positions, size_t
   return (float)(positions ? positions[tok] : (int)(tok % T));
 }
 
-// cos and sin of the token's angles for the lane's dims 8 dl .. 8 dl + 7:
-// lanes j and j + 32 evaluate angle j = f32(position) * freq[j] (freq is
-// the lane's freq[lane mod 32]), and each
-// lane reads its dims' angles (d mod 32) by shuffle.  The fused forward's
-// rope table evaluates the same sincosf of the same product.
+// cos and sin of the token's angles for the lane's dims 8 dl .. 8 dl + 7.
+// `freq` is the lane's freq[lane mod 32], so lanes j and j + 32 evaluate
+// angle j = f32(position) * freq[j]; each lane reads its dims' angles
+// (d mod 32) by shuffle.  The fused forward's rope table evaluates the same
+// sincosf of the same product.
 template <bool F32>
 __device__ __forceinline__ void token_cos_sin(float pos, float freq, int dl, float (&c)[8],
                                               float (&s)[8]) {
