@@ -181,3 +181,28 @@ def test_product_path_refuses_host_tensors():
         bidirectional.attention(q, q, q, m, m)
     with pytest.raises(ValueError, match="GPU only"):
         attention.dense_cached_attention(q[:, :1], q, q, 2)
+
+
+def test_last_error_is_per_thread():
+    """mf_last_error reports the calling thread's own failure while other threads fail
+    differently in between (ctypes drops the GIL around each call, so the C calls interleave)."""
+    import threading
+
+    cases = {0: (dict(d=128), "head_dim 128"), 1: (dict(hq=3), "divisible by KV heads")}
+    start = threading.Barrier(2)
+    wrong = []
+
+    def worker(i):
+        kw, text = cases[i]
+        start.wait()
+        for _ in range(2000):
+            assert _fwd(**kw) != 0
+            if text not in _msg():
+                wrong.append((i, _msg()))
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not wrong, wrong[:3]
