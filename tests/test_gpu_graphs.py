@@ -69,3 +69,43 @@ def test_captured_step_replays_equal_eager(mode, device):
             same = torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a.view(torch.int16),
                                r.view(torch.int32) if r.dtype == torch.float32 else r.view(torch.int16))
             assert same, (trial, name)
+
+
+def _problem(seed, mode, device):
+    rng = np.random.default_rng(seed)
+    b, t, hq, hkv, d = 2, 777, 8, 2, 64
+    seg_np = np.zeros((b, t), np.int32)
+    for row in range(b):
+        pos, sid = 0, 1
+        while pos < t:
+            n = int(rng.integers(10, 300))
+            seg_np[row, pos:pos + n] = sid
+            pos, sid = pos + n, sid + 1
+    seg = torch.tensor(seg_np, device=device)
+    mask = (seg != 0).to(torch.int32)
+    g = torch.Generator(device=device).manual_seed(seed)
+    mk = lambda h: torch.randn(b, t, h, d, generator=g, device=device).to(torch.bfloat16)  # noqa: E731
+    return mk(hq), mk(hkv), mk(hkv), mk(hq), seg, mask, mode
+
+
+def test_two_streams_at_once_equal_serial_calls(device):
+    """The library keeps no state between calls: two problems launched alternately on two
+    streams (default priority) while both are in flight give what serial calls give, bit for
+    bit."""
+    say("two streams")
+    probs = [_problem(21, 0, device), _problem(22, 1, device)]
+    serial = [_step(*p) for p in probs]
+    torch.cuda.synchronize(device)
+    streams = [torch.cuda.Stream(device) for _ in probs]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(device))
+    results = [[], []]
+    for _ in range(3):
+        for i, (p, s) in enumerate(zip(probs, streams)):
+            with torch.cuda.stream(s):
+                results[i].append(_step(*p))
+    torch.cuda.synchronize(device)
+    for i in range(2):
+        for rep in results[i]:
+            for name, a, r in zip(("out", "lse", "dq", "dk", "dv"), rep, serial[i]):
+                assert torch.equal(a, r), (i, name)
