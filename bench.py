@@ -29,8 +29,8 @@
   mean segment 512) and C5 (1 x 32768, segments of 16-128 tokens): ms per
   step, useful TFLOP/s and the fraction of the max(MFMA, HBM) roofline time.
 
-The decode, the rows and C3/C5 are measured before the C2 step, so the GPU's
-clocks are at their steady state when the headline is timed.
+The decode, the rows, C5 and then C3 are measured before the C2 step, so the
+GPU's clocks are near their steady state when the headline is timed.
 ``--config C3`` or ``--config C5`` (or ``--config C2 --step-only``) prints one of
 those step lines alone.
 
@@ -593,11 +593,14 @@ def main() -> int:
                           "step_roofline": gpu["step_roofline"]}))
         return 0
     # The other measurements run first: their GPU work also brings the clocks to
-    # their steady state before the headline C2 step is timed.
+    # their steady state before the headline C2 step is timed.  C3, the heaviest
+    # of them, runs last: after a lighter load the C2 step slows for its first
+    # ~30 steps while the clocks settle (one box, per-step times: ~700 us at steps
+    # 4-9, ~615 us from step 35), less so right after C3.
     decode = decode_leg(args.steps, args.warmup)
     rows = rows_leg(args.steps)
     configs = {}
-    for name in ("C3", "C5"):
+    for name in ("C5", "C3"):
         other = gpu_leg(args.steps, args.warmup, name=name, decode=False)
         configs[name] = {"workload": other["config"]["workload"],
                          "ms_per_step": other["ms_per_step"],
