@@ -356,6 +356,52 @@ def test_large_logits_and_rising_maxima(mode, dtype, device):
             check_bf16_sum(f"large logits mode {mode} {name}", a, r, mags[i] + np.abs(r))
 
 
+@pytest.mark.parametrize("b, t, s, hq, hkv, seed", [(1, 286, 3, 6, 2, 5030), (3, 315, 10, 3, 1, 5472)])
+def test_few_keys_many_queries(b, t, s, hq, hkv, seed, device):
+    """Key-mask mode with 3-10 keys for ~300 queries (shapes a randomized sweep found): every dV
+    element sums ~900 products P dO with P near 1/2, so bf16 effects that are relative 2**-9
+    per term add up beyond the element-wise bf16 bar against FP64 (0.13 at |dV| ~ 37).  They
+    are pinned exactly: the forward's lse is the log of the sum of the bf16-rounded
+    probabilities (`v_dot2` row sums), and dV is bf16(sum over queries and heads of
+    bf16(exp(s - lse)) dO) bit for bit (at most one bf16 ulp where P sits on a rounding
+    boundary); every output is within what those roundings can move it from FP64."""
+    rng = np.random.default_rng(seed)
+    say("few keys", (b, t, s, hq, hkv))
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, torch.bfloat16, 0.6, s=s)
+    mask = (rng.random((b, s)) > 0.25).astype(np.int32)
+    mask[:, 0] = 1
+    plan = ops.block_map(None, torch.tensor(mask, device=device), 2, t, s)
+    out, lse = ops.attn_fwd(q, k, v, plan, 2, 0.125)
+    dq, dk, dv = ops.attn_bwd(q, k, v, out, do, lse, plan, 2, 0.125)
+    q64, k64, do64 = (x.double().cpu() for x in (q, k, do))
+    g = hq // hkv
+    log2e = 1.4426950408889634
+    x = torch.einsum("bthd,bshd->bhts", q64, k64.repeat_interleave(g, dim=2)) * (0.125 * log2e)
+    x = x.masked_fill(~torch.tensor(mask, dtype=torch.bool)[:, None, None, :], float("-inf"))
+    bf = lambda y: y.float().to(torch.bfloat16).double()  # noqa: E731
+    shift = x.max(-1, keepdim=True).values
+    lse2_rounded_sums = shift + torch.log2(bf(torch.exp2(x - shift)).sum(-1, keepdim=True))
+    lse2 = lse.double().cpu()[..., None] * log2e
+    assert (lse2 - lse2_rounded_sums).abs().max().item() < 1e-5
+    pb = bf(torch.exp2(x - lse2))
+    dv_model = torch.einsum("bhts,bthd->bshd", pb, do64).reshape(b, s, hkv, g, 64).sum(3)
+    terms = torch.einsum("bhts,bthd->bshd", pb, do64.abs()).reshape(b, s, hkv, g, 64).sum(3)
+    ulps = (dv.cpu().view(torch.int16).int() - dv_model.float().to(torch.bfloat16).view(torch.int16).int()).abs()
+    # where the sum cancels, the kernel's fp32 accumulation of ~900 terms (at most 2**-14 of
+    # their magnitude sum) can move the small result by more than one of its bf16 ulps
+    acc_ok = (dv.cpu().double() - dv_model).abs() <= 2.0 ** -8 * dv_model.abs() + 2.0 ** -14 * terms
+    odd = ulps > 1
+    say(f"few keys dV against the bf16 model: {int((ulps == 0).sum())} of {ulps.numel()} identical, "
+        f"{int(odd.sum())} beyond one ulp at |dV| <= {dv_model.abs()[odd].max().item() if odd.any() else 0:.3g} "
+        f"(term sums {terms[odd].min().item() if odd.any() else 0:.3g}+)")
+    assert bool((~odd | acc_ok).all()) and float((ulps == 0).float().mean()) > 0.99
+    ref = oatt.grouped_fp64(2, *(x_.float().cpu().numpy() for x_ in (q, k, v)), mask, None,
+                            d_out=do.float().cpu().numpy())
+    mags = _rounding_magnitudes(2, *(x_.float().cpu().numpy() for x_ in (q, k, v, do)), mask, None)
+    for i, (name, a_, r) in enumerate(zip(("out", "dq", "dk", "dv"), (out, dq, dk, dv), ref)):
+        check_bf16_sum(f"few keys {name}", a_, r, mags[i] + np.abs(r))
+
+
 @pytest.mark.parametrize("hq, hkv", [(4, 4), (8, 2), (6, 2), (3, 1), (16, 2), (2, 2)])
 @pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
 @pytest.mark.parametrize("mode", [0, 1])
