@@ -6,7 +6,7 @@ Test infrastructure only (the product never imports ``oracle``).
   (fp32 statistics; the normalised value is cast to the tensor dtype before
   the gain multiply).
 * ``apply_rotary`` follows ``kernels/rotary.py:7-39``: single-precision
-  frequencies ``theta ** (-arange(0, D, 2) / D)`` and angles
+  frequencies ``theta ** (-arange(0, D, 2) / D)`` (correctly rounded) and angles
   ``f32(position) * freq``, split-half rotation ``(-x[D/2:], x[:D/2])``.
   Evaluated in float64 from those single-precision angles.
 * ``rotate_pairs`` is an independent restatement: a 2x2 rotation matrix per
@@ -44,9 +44,11 @@ def rms_norm(x, weight, eps: float):
 
 
 def frequencies(rope_theta: float, head_dim: int) -> np.ndarray:
-    """``rope_theta ** (-arange(0, D, 2) / D)`` in float32 (rotary.py:33-35)."""
-    exps = -(np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim))
-    return (np.float32(rope_theta) ** exps).astype(np.float32)
+    """``rope_theta ** (-arange(0, D, 2) / D)`` in float32 (rotary.py:33-35), correctly
+    rounded: the float64 power rounded once.  (NumPy's float32 power is up to ~0.9 ulp off,
+    and a one-ulp frequency difference moves the angle of position p by p * 6e-8 of it.)"""
+    exps = -(np.arange(0, head_dim, 2, dtype=np.float64) / head_dim)
+    return (np.float64(np.float32(rope_theta)) ** exps).astype(np.float32)
 
 
 def angles(positions, rope_theta: float, head_dim: int) -> np.ndarray:

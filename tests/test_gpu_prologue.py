@@ -240,3 +240,31 @@ def test_fused_query_prologue_at_the_layer_level(device):
     with pytest.raises(ValueError, match="no backward"):
         prologue.packed_attention_normed_query(q_raw.requires_grad_(), kn, v, qg, mask, seg, pos,
                                                eps=1e-6, rope_theta=1e6)
+
+
+@pytest.mark.parametrize("hq, hkv", [(37, 5), (40, 16), (3, 1)])
+def test_large_positions_and_head_counts(hq, hkv, device):
+    """fp32 at 1e-5 against the FP64 prologue and its VJP with positions up to 2**20 (where a
+    one-ulp difference in a rotary frequency would move an angle by ~0.06 rad: the kernel's
+    host-side frequencies are the correctly rounded single-precision powers, as the oracle's)
+    and head counts that are not multiples of 8 or exceed four 8-head groups per token (the
+    forward loads a token's groups in batches of four, the backward in batches of three)."""
+    rng = np.random.default_rng(100 + hq)
+    b, t, d = 2, 61, 64
+    say("prologue positions to 2**20", hq, hkv)
+    pos = rng.integers(0, 1 << 20, size=(b, t)).astype(np.int32)
+    q = (rng.standard_normal((b, t, hq, d)) * 2).astype(np.float32)
+    k = (rng.standard_normal((b, t, hkv, d)) * 2).astype(np.float32)
+    qg, kg = (1 + 0.1 * rng.standard_normal((2, d))).astype(np.float32)
+    gq, gk = rng.standard_normal((b, t, hq, d)).astype(np.float32), rng.standard_normal((b, t, hkv, d)).astype(np.float32)
+    tq, tk = (torch.tensor(x, device=device).requires_grad_(True) for x in (q, k))
+    tqg, tkg = (torch.tensor(x, device=device).requires_grad_(True) for x in (qg, kg))
+    oq, ok = prologue.qk_norm_rope(tq, tk, tqg, tkg, torch.tensor(pos), eps=1e-5, rope_theta=1e4)
+    torch.autograd.backward((oq, ok), (torch.tensor(gq, device=device), torch.tensor(gk, device=device)))
+    rq, rk = oprol.qk_norm_rope(q, k, qg, kg, pos, 1e-5, 1e4)
+    vjp = oprol.qk_norm_rope_vjp(*(x.astype(np.float64) for x in (q, k, qg, kg)), pos, 1e-5, 1e4,
+                                 gq.astype(np.float64), gk.astype(np.float64))
+    got = (oq, ok, tq.grad, tk.grad, tqg.grad, tkg.grad)
+    for name, a, r in zip(("q", "k", "dq", "dk", "dq_gain", "dk_gain"), got, (rq, rk, *vjp)):
+        scale = max(1.0, float(np.abs(r).max()))
+        np.testing.assert_allclose(a.detach().cpu().numpy(), r, rtol=1e-5, atol=1e-5 * scale, err_msg=name)

@@ -1,6 +1,7 @@
 """The prologue oracle (QK RMS norm + rotary, packer positions) pinned on the CPU."""
 
 import numpy as np
+import pytest
 
 from oracle import packing, prologue
 
@@ -35,10 +36,13 @@ def test_rotation_keeps_pair_norms_and_depends_on_relative_position():
     assert abs(rq(40) @ rk(10) - rq(30) @ rk(0)) < 1e-4
 
 
-def test_frequencies_are_single_precision_powers():
-    f = prologue.frequencies(10000.0, 64)
+@pytest.mark.parametrize("theta", [500.0, 10000.0, 1000000.0])
+def test_frequencies_are_correctly_rounded_single_precision_powers(theta):
+    f = prologue.frequencies(theta, 64)
+    exact = np.float64(theta) ** (-np.arange(0, 64, 2) / 64)
     assert f.dtype == np.float32 and f[0] == 1.0
-    np.testing.assert_allclose(f, 10000.0 ** (-np.arange(0, 64, 2) / 64), rtol=1e-6)
+    # within half a float32 ulp of the exact power: the nearest single-precision value
+    assert bool((np.abs(f.astype(np.float64) - exact) <= 0.5 * np.spacing(f).astype(np.float64)).all())
 
 
 def test_rms_norm_closed_form():
