@@ -219,6 +219,50 @@ def test_randomized_shapes(seed, device):
             check_bf16(f"randomized {seed} {name}", a, r)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_randomized_multi_tile(seed, device):
+    """Seeded random calls at multi-tile lengths: 400-5000 tokens (key lengths of their own in
+    the key-mask mode), segments of 1-2048 tokens with padding and ids from -4 upward, 1-8 KV
+    heads with G up to 8, bf16 forward and backward against the fp32 reference at the
+    element-wise bf16 bar."""
+    rng = np.random.default_rng(90000 + seed)
+    mode = int(rng.integers(0, 3))
+    b, t = int(rng.integers(1, 4)), int(rng.integers(400, 5001))
+    s = int(rng.integers(64, 5001)) if mode == 2 else t
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    hq = min(hkv * int(rng.choice([1, 2, 3, 4, 8])), 32)
+    say("randomized multi-tile", seed, mode, (b, t, s, hq, hkv))
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, torch.bfloat16, 0.6, s=s)
+    if mode == 2:
+        mask = (rng.random((b, s)) > rng.uniform(0.05, 0.9)).astype(np.int32)
+        mask[:, 0] = 1
+        seg = None
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, torch.tensor(mask, device=device))  # noqa: E731
+    else:
+        seg = np.zeros((b, t), np.int32)
+        for r in range(b):
+            pos, sid = 0, int(rng.integers(-5, 3))
+            while pos < t:
+                n = int(rng.integers(1, 91)) if rng.random() < 0.6 else int(rng.integers(91, 2049))
+                sid += 1
+                sid += sid == 0
+                seg[r, pos:pos + n] = 0 if rng.random() < 0.1 else sid
+                pos += n
+        mask = (rng.random((b, t)) > 0.05).astype(np.int32)
+        tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+        if mode == 0:
+            fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+        else:
+            fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = torch_reference(mode, q, k, v, mask, seg, do)
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        diff = (a.float() - r).abs()
+        raw, excess = diff.max().item(), (diff - BF16_HALF_ULP * r.abs()).max().item()
+        say(f"randomized multi-tile {seed} {name}: max-abs {raw:.3e} beyond-rounding {excess:.3e}")
+        assert excess < BF16_TOL, (name, raw, excess)
+
+
 def _chunked_row(rng, t):
     """One row of ``t`` tokens cut into chunks of 128-token multiples (up to 4096 tokens), each
     filled with whole segments of 16-128 tokens (one in eight of 129-4096, cut at the chunk's
