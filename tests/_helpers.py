@@ -29,9 +29,9 @@ def operands(rng: np.random.Generator, b, t, hq, hkv, d, dtype, scale=1.0, s=Non
     return q, k, v, do
 
 
-def torch_reference(mode, q, k, v, mask, seg, do):
-    """fp32 forward and gradients, one id group at a time (GPU)."""
-    qf, kf, vf, dof = (x.float() for x in (q, k, v, do))
+def torch_reference(mode, q, k, v, mask, seg, do, dtype=torch.float32):
+    """Forward and gradients in ``dtype`` (fp32 by default), one id group at a time (GPU)."""
+    qf, kf, vf, dof = (x.to(dtype) for x in (q, k, v, do))
     b, t, hq, d = qf.shape
     hkv = kf.shape[2]
     g = hq // hkv

@@ -263,6 +263,49 @@ def test_randomized_multi_tile(seed, device):
         assert excess < BF16_TOL, (name, raw, excess)
 
 
+@pytest.mark.parametrize("seed", range(4))
+def test_randomized_multi_tile_fp32(seed, device):
+    """The fp32 kernels at multi-tile lengths (400-3000 tokens, three modes, segments of
+    1-2048 tokens, G up to 4) against the per-group reference in float64: rtol 1e-5 with the
+    absolute term scaled by the tensor's largest magnitude, since dK/dV sum up to ~10^4 terms
+    whose fp32 accumulation moves a cancelled element by ~1e-5 absolute."""
+    rng = np.random.default_rng(95000 + seed)
+    mode = int(rng.integers(0, 3))
+    b, t = int(rng.integers(1, 3)), int(rng.integers(400, 3001))
+    s = int(rng.integers(64, 3001)) if mode == 2 else t
+    hkv = int(rng.choice([1, 2, 4]))
+    hq = hkv * int(rng.choice([1, 2, 3, 4]))
+    say("randomized multi-tile fp32", seed, mode, (b, t, s, hq, hkv))
+    q, k, v, do = operands(rng, b, t, hq, hkv, 64, torch.float32, 0.6, s=s)
+    if mode == 2:
+        mask = (rng.random((b, s)) > rng.uniform(0.05, 0.9)).astype(np.int32)
+        mask[:, 0] = 1
+        seg = None
+        fn = lambda a, bb, c: bidirectional.attention(a, bb, c, torch.tensor(mask, device=device))  # noqa: E731
+    else:
+        seg = np.zeros((b, t), np.int32)
+        for r in range(b):
+            pos, sid = 0, 1
+            while pos < t:
+                n = int(rng.integers(1, 91)) if rng.random() < 0.6 else int(rng.integers(91, 2049))
+                seg[r, pos:pos + n] = 0 if rng.random() < 0.1 else sid
+                sid += 1
+                pos += n
+        mask = (rng.random((b, t)) > 0.05).astype(np.int32)
+        tm, ts = torch.tensor(mask, device=device), torch.tensor(seg, device=device)
+        if mode == 0:
+            fn = lambda a, bb, c: attention.dense_packed_causal_attention(a, bb, c, tm, ts)  # noqa: E731
+        else:
+            fn = lambda a, bb, c: bidirectional.attention(a, bb, c, tm, ts)  # noqa: E731
+    got = _grads(fn, q, k, v, do)
+    ref = torch_reference(mode, q, k, v, mask, seg, do, dtype=torch.float64)
+    for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+        scale = max(1.0, r.abs().max().item())
+        excess = ((a.double() - r).abs() - 1e-5 * r.abs()).max().item()
+        say(f"randomized multi-tile fp32 {seed} {name}: beyond rtol {excess:.3e} (atol {1e-5 * scale:.2e})")
+        assert excess <= 1e-5 * scale, (name, excess)
+
+
 def _chunked_row(rng, t):
     """One row of ``t`` tokens cut into chunks of 128-token multiples (up to 4096 tokens), each
     filled with whole segments of 16-128 tokens (one in eight of 129-4096, cut at the chunk's
