@@ -239,30 +239,51 @@ struct ConvBwdArgs {
 
 constexpr int kConvBwdTile = 16;    // output tokens per thread of the backward
 constexpr int kConvBwdTiles = 32;   // token tiles per workgroup
-constexpr int kConvBwdChunks = 8;   // 8-channel chunks per workgroup
+constexpr int kConvBwdChunks = 8;   // channel chunks per workgroup
 
-template <typename T>
-__device__ __forceinline__ void load8(const T* p, float (&x)[8]) {
-  Raw8<T> r;
-  r.load(p);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) x[e] = r[e];
+// Channels per thread of the backward.  A thread holds a ring of W + 1 slots
+// of four input rows (W = 2K - 1 causal, K or K + 1 centered) plus K taps and
+// K tap gradients per channel.  At 8 channels that exceeds the register file
+// beyond K = 4 (K = 5 centered still fits): the compiler spilled up to 2 KB
+// per lane to scratch, 4-6x slower, so wider filters take 4 channels.
+template <typename T, int K, bool CENTERED>
+constexpr int conv_bwd_channels() {
+  return K <= 4 || (K == 5 && CENTERED && !std::is_same<T, float>::value) ? 8 : 4;
 }
 
-template <typename T>
-__device__ __forceinline__ void store8(T* p, const float (&x)[8]) {
+// CW elements of one token row of the backward as loaded.
+template <typename T, int CW>
+struct RawC : Raw8<T> {};
+template <>
+struct RawC<bf16, 4> {
+  bf16x4 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x4*>(p); }
+  __device__ __forceinline__ float operator[](int e) const { return (float)v[e]; }
+};
+template <>
+struct RawC<float, 4> {
+  f32x4 v;
+  __device__ __forceinline__ void load(const float* p) { v = *reinterpret_cast<const f32x4*>(p); }
+  __device__ __forceinline__ float operator[](int e) const { return v[e]; }
+};
+
+template <typename T, int CW>
+__device__ __forceinline__ void store_row(T* p, const float (&x)[CW]) {
   if constexpr (std::is_same<T, float>::value) {
-    f32x4 lo, hi;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) lo[e] = x[e], hi[e] = x[4 + e];
-    *reinterpret_cast<f32x4*>(p) = lo;
-    *reinterpret_cast<f32x4*>(p + 4) = hi;
-  } else {
+    for (int h = 0; h < CW; h += 4) {
+      const f32x4 v = {x[h], x[h + 1], x[h + 2], x[h + 3]};
+      *reinterpret_cast<f32x4*>(p + h) = v;
+    }
+  } else if constexpr (CW == 8) {
     uint32_t words[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) words[e / 2] = pack_pair(x[e], x[e + 1]);
     const u32x4 v = {words[0], words[1], words[2], words[3]};
     *reinterpret_cast<u32x4*>(p) = v;
+  } else {
+    const u32x2 v = {pack_pair(x[0], x[1]), pack_pair(x[2], x[3])};
+    *reinterpret_cast<u32x2*>(p) = v;
   }
 }
 
@@ -273,9 +294,9 @@ __device__ __forceinline__ void store8(T* p, const float (&x)[8]) {
 // width) kAhead steps before it is used; at step q output q - (W - 1) is
 // formed from the W newest slots, so every row is loaded once per thread.
 // The step loop is unrolled by R, so all slot indices are compile-time.
-template <typename T, int K, int LO>
+template <typename T, int K, int LO, int CW>
 __device__ __forceinline__ void conv_bwd_tile(const ConvBwdArgs& a, size_t row, int t0, int c0,
-                                              const float (&w)[K][8], float (&dw)[K][8]) {
+                                              const float (&w)[K][CW], float (&dw)[K][CW]) {
   constexpr bool kBf16 = !std::is_same<T, float>::value;
   constexpr int SMIN = LO < -LO - (K - 1) ? LO : -LO - (K - 1);
   constexpr int SMAX = LO + K - 1 > -LO ? LO + K - 1 : -LO;
@@ -287,7 +308,7 @@ __device__ __forceinline__ void conv_bwd_tile(const ConvBwdArgs& a, size_t row, 
   const T* bp = reinterpret_cast<const T*>(a.b);
   const T* cp = reinterpret_cast<const T*>(a.c);
   const T* gp = reinterpret_cast<const T*>(a.g);
-  Raw8<T> rv[R], rb[R], rg[R], rc[R];
+  RawC<T, CW> rv[R], rb[R], rg[R], rc[R];
   int sg[R];
   auto issue = [&](int q, int slot) {
     const int s = t0 + SMIN + q;
@@ -315,9 +336,9 @@ __device__ __forceinline__ void conv_bwd_tile(const ConvBwdArgs& a, size_t row, 
       auto slot = [&](int d) { return ((k - SMAX + d) % R + R) % R; };  // input at t + d
       const int s0 = slot(0);
       const int me = sg[s0];
-      float m[8], du[8], h0[8];
+      float m[CW], du[CW], h0[CW];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
+      for (int e = 0; e < CW; ++e) {
         m[e] = 0.f;
         du[e] = 0.f;
         h0[e] = a.c ? rg[s0][e] * rc[s0][e] : rg[s0][e];
@@ -329,7 +350,7 @@ __device__ __forceinline__ void conv_bwd_tile(const ConvBwdArgs& a, size_t row, 
         const int su = slot(LO + i), sh = slot(-LO - i);
         if (me != 0 && sg[su] == me) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
+          for (int e = 0; e < CW; ++e) {
             float u = rv[su][e];
             if (a.b) u = kBf16 ? round_bf16(u * rb[su][e]) : u * rb[su][e];
             const float p = u * w[i][e];
@@ -339,7 +360,7 @@ __device__ __forceinline__ void conv_bwd_tile(const ConvBwdArgs& a, size_t row, 
         }
         if (me != 0 && sg[sh] == me) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
+          for (int e = 0; e < CW; ++e) {
             const float hn = a.c ? rg[sh][e] * rc[sh][e] : rg[sh][e];
             du[e] = fmaf(hn, w[i][e], du[e]);
           }
@@ -347,30 +368,31 @@ __device__ __forceinline__ void conv_bwd_tile(const ConvBwdArgs& a, size_t row, 
       }
       const size_t off = (row + t0 + j) * a.C + c0;
       if (a.dc) {
-        float dc[8];
+        float dc[CW];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dc[e] = rg[s0][e] * m[e];
-        store8<T>(reinterpret_cast<T*>(a.dc) + off, dc);
+        for (int e = 0; e < CW; ++e) dc[e] = rg[s0][e] * m[e];
+        store_row<T, CW>(reinterpret_cast<T*>(a.dc) + off, dc);
       }
-      float dv[8];
+      float dv[CW];
       if (a.b) {
-        float db[8];
+        float db[CW];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dv[e] = du[e] * rb[s0][e], db[e] = du[e] * rv[s0][e];
-        store8<T>(reinterpret_cast<T*>(a.db) + off, db);
+        for (int e = 0; e < CW; ++e) dv[e] = du[e] * rb[s0][e], db[e] = du[e] * rv[s0][e];
+        store_row<T, CW>(reinterpret_cast<T*>(a.db) + off, db);
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dv[e] = du[e];
+        for (int e = 0; e < CW; ++e) dv[e] = du[e];
       }
-      store8<T>(reinterpret_cast<T*>(a.dv) + off, dv);
+      store_row<T, CW>(reinterpret_cast<T*>(a.dv) + off, dv);
     }
   }
 }
 
 template <typename T, int K, bool CENTERED>
 __global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) {
-  __shared__ float red[4][kConvBwdChunks][K * 8];
-  const int chunks = a.C / 8;
+  constexpr int CW = conv_bwd_channels<T, K, CENTERED>();
+  __shared__ float red[4][kConvBwdChunks][K * CW];
+  const int chunks = a.C / CW;
   const int tiles = (a.T + kConvBwdTile - 1) / kConvBwdTile;
   const int cgroups = (chunks + kConvBwdChunks - 1) / kConvBwdChunks;
   const int tgroups = (tiles + kConvBwdTiles - 1) / kConvBwdTiles;
@@ -381,23 +403,23 @@ __global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) 
   const int ch = cg * kConvBwdChunks + lc;
   const int tile = tg * kConvBwdTiles + lt;
   const bool on = ch < chunks && tile < tiles;
-  const int c0 = min(ch, chunks - 1) * 8;
+  const int c0 = min(ch, chunks - 1) * CW;
   const size_t row = (size_t)b * a.T;
 
-  float w[K][8];
+  float w[K][CW];
 #pragma unroll
   for (int i = 0; i < K; ++i)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w[i][e] = (float)reinterpret_cast<const T*>(a.w)[(size_t)(c0 + e) * K + i];
-  float dw[K][8];
+    for (int e = 0; e < CW; ++e) w[i][e] = (float)reinterpret_cast<const T*>(a.w)[(size_t)(c0 + e) * K + i];
+  float dw[K][CW];
 #pragma unroll
   for (int i = 0; i < K; ++i)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dw[i][e] = 0.f;
+    for (int e = 0; e < CW; ++e) dw[i][e] = 0.f;
 
   if (on) {
     const int t0 = tile * kConvBwdTile;
-    conv_bwd_tile<T, K, CENTERED ? -(K / 2) : -(K - 1)>(a, row, t0, c0, w, dw);
+    conv_bwd_tile<T, K, CENTERED ? -(K / 2) : -(K - 1), CW>(a, row, t0, c0, w, dw);
   }
   // tap gradients: add the 8 tiles of each wave (lanes lc, lc + 8, ... hold
   // the same channels), then the 4 waves, in a fixed order
@@ -405,20 +427,20 @@ __global__ __launch_bounds__(256) void segmented_conv_bwd_kernel(ConvBwdArgs a) 
 #pragma unroll
   for (int i = 0; i < K; ++i)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < CW; ++e) {
       float x = dw[i][e];
       x += __shfl_xor(x, 8);
       x += __shfl_xor(x, 16);
       x += __shfl_xor(x, 32);
-      if (lane < kConvBwdChunks) red[wave][lane][i * 8 + e] = x;
+      if (lane < kConvBwdChunks) red[wave][lane][i * CW + e] = x;
     }
   __syncthreads();
-  for (int j = threadIdx.x; j < kConvBwdChunks * K * 8; j += blockDim.x) {
-    const int jc = j / (K * 8), ie = j % (K * 8), i = ie / 8, e = ie % 8;
+  for (int j = threadIdx.x; j < kConvBwdChunks * K * CW; j += blockDim.x) {
+    const int jc = j / (K * CW), ie = j % (K * CW), i = ie / CW, e = ie % CW;
     const int chj = cg * kConvBwdChunks + jc;
     if (chj >= chunks) continue;
     const float x = ((red[0][jc][ie] + red[1][jc][ie]) + red[2][jc][ie]) + red[3][jc][ie];
-    a.partials[((size_t)(b * tgroups + tg) * a.C + chj * 8 + e) * K + i] = x;
+    a.partials[((size_t)(b * tgroups + tg) * a.C + chj * CW + e) * K + i] = x;
   }
 }
 
@@ -456,18 +478,23 @@ size_t conv_bwd_workspace_bytes(int B, int T, int C, int K) {
 
 template <typename T>
 hipError_t launch_conv_bwd_t(const ConvBwdArgs& a, hipStream_t stream) {
-  const int chunks = a.C / 8;
   const int tiles = (a.T + kConvBwdTile - 1) / kConvBwdTile;
-  const long long blocks = (long long)a.B * ((tiles + kConvBwdTiles - 1) / kConvBwdTiles) *
-                           ((chunks + kConvBwdChunks - 1) / kConvBwdChunks);
-  const dim3 grid((unsigned)blocks);
+  const long long tgroups = (tiles + kConvBwdTiles - 1) / kConvBwdTiles;
+  // one workgroup per (row, tile group, group of kConvBwdChunks channel chunks)
+  auto grid_for = [&](int cw) {
+    const int chunks = a.C / cw;
+    return dim3((unsigned)(a.B * tgroups * ((chunks + kConvBwdChunks - 1) / kConvBwdChunks)));
+  };
 #define MF_CONV_BWD_CASE(KK)                                                                     \
-    case KK:                                                                                      \
+    case KK: {                                                                                    \
       if (a.centered)                                                                             \
-        hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, KK, true>), grid, dim3(256), 0, stream, a); \
+        hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, KK, true>),                              \
+                           grid_for(conv_bwd_channels<T, KK, true>()), dim3(256), 0, stream, a);  \
       else                                                                                        \
-        hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, KK, false>), grid, dim3(256), 0, stream, a); \
-      break;
+        hipLaunchKernelGGL((segmented_conv_bwd_kernel<T, KK, false>),                             \
+                           grid_for(conv_bwd_channels<T, KK, false>()), dim3(256), 0, stream, a); \
+      break;                                                                                      \
+    }
   switch (a.K) {
     MF_CONV_BWD_CASE(1)
     MF_CONV_BWD_CASE(2)

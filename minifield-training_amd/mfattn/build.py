@@ -36,6 +36,11 @@ FLAGS = [
     # every threadIdx/blockIdx/blockDim read, rsqrtf and sincosf into a call
     # (a stack frame, and a wait for every load in flight at each call)
     "-fno-honor-nans",
+    # the conv backward's ring loop (2K steps, slot indices compile-time only
+    # when it is fully unrolled) exceeds the default size limit for pragma
+    # unrolls at K >= 7 in bf16; a partial unroll left its ring arrays in
+    # scratch memory.  No other loop here reaches the limit.
+    "-mllvm", "-pragma-unroll-threshold=65536",
     "-Wall",
     "-Wno-unused-function",
 ]

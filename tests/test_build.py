@@ -48,13 +48,14 @@ def _code_objects(lib: pathlib.Path, tmp: pathlib.Path):
         yield co
 
 
-def test_device_code_makes_no_calls(tmp_path):
+def _disassembly(tmp_path):
+    """Instruction lines of every gfx950 function in the library, by symbol."""
     if not _lib.LIB_PATH.exists():
         pytest.skip("libmfattn.so is not built")
     missing = [t for t in TOOLS if _tool(t) is None]
     if missing:
         pytest.skip(f"ROCm LLVM tools missing: {missing}")
-    kernels, calls = set(), []
+    funcs = {}
     for co in _code_objects(_lib.LIB_PATH, tmp_path):
         dis = subprocess.run([_tool("llvm-objdump"), "-d", "--mcpu=gfx950", str(co)],
                              capture_output=True, text=True, check=True).stdout
@@ -63,10 +64,29 @@ def test_device_code_makes_no_calls(tmp_path):
             m = re.match(r"^[0-9a-f]+ <(\S+)>:", line)
             if m:
                 current = m.group(1)
-                kernels.add(current)
-            elif "s_swappc_b64" in line:
-                calls.append(current)
-    assert any(k.startswith("_ZN2mf20attn_fwd_bf16_kernel") for k in kernels), sorted(kernels)[:5]
-    assert not calls, sorted(set(calls))
+                funcs.setdefault(current, [])
+            elif current is not None and line.strip():
+                funcs[current].append(line)
+    assert any(k.startswith("_ZN2mf20attn_fwd_bf16_kernel") for k in funcs), sorted(funcs)[:5]
+    return funcs
+
+
+def test_device_code_makes_no_calls(tmp_path):
+    funcs = _disassembly(tmp_path)
+    calls = sorted(k for k, lines in funcs.items() if any("s_swappc_b64" in l for l in lines))
+    assert not calls, calls
     # nothing but kernels: no out-of-line device-library function was emitted
-    assert not [k for k in kernels if k.startswith("__o")], sorted(k for k in kernels if k.startswith("__o"))
+    assert not [k for k in funcs if k.startswith("__o")], sorted(k for k in funcs if k.startswith("__o"))
+
+
+def test_scratch_is_one_spill_outside_the_key_loop(tmp_path):
+    """Register spills go to scratch memory in HBM.  The forward with the query's norm and
+    RoPE fused in keeps one register there across its key loop (one store before, one load
+    after); no other kernel touches scratch."""
+    funcs = _disassembly(tmp_path)
+    use = {k: [l for l in lines if "scratch_" in l] for k, lines in funcs.items()}
+    use = {k: v for k, v in use.items() if v}
+    fused = [k for k in use if k.startswith("_ZN2mf20attn_fwd_bf16_kernelILi2ELb1E")]
+    assert set(use) <= set(fused), sorted(set(use) - set(fused))
+    for k in fused:
+        assert len(use[k]) <= 2, (k, use[k])
