@@ -475,7 +475,7 @@ TRAFFIC_KERNELS = {
     "attn_fwd": (("mf::attn_fwd_bf16_kernel<2, false>", "mf::attn_fwd_bf16_kernel<1, false>"),
                  "C2", None),
     "attn_bwd_dq": (("mf::bwd_dq_bf16_kernel<",), "C2", None),  # computes D itself in the product call
-    "attn_bwd_dkdv": (("mf::bwd_dkdv_bf16_kernel<",), "C2", None),
+    "attn_bwd_dkdv": (("mf::bwd_dkdv_bf16_kernel",), "C2", None),
     "decode": (("mf::decode_prep_kernel", "mf::decode_rows_kernel<", "mf::decode_bf16_kernel<",
                 "mf::decode_combine_kernel<"), "C4", 0),
     "decode_append": (("mf::decode_rows_kernel<", "mf::decode_bf16_kernel<",

@@ -4,8 +4,11 @@
  * allocation happens inside any entry point; callers pass every buffer,
  * including the plan and workspace whose sizes the *_bytes queries return.
  * Every entry point is stream-ordered on `stream` (a hipStream_t, NULL =
- * default stream), never synchronises the host, and keeps no mutable global
- * state, so it is safe to call from several host threads.
+ * default stream) and never synchronises the host.  Every entry point but
+ * mf_decode_static keeps no mutable global state, so it is safe to call
+ * from several host threads; mf_decode_static keeps its workspace in one
+ * library-owned device array per GPU (and a per-device table of its
+ * address), so its calls on one GPU race unless ordered on one stream.
  *
  * Status: 0 on success, a negative MF_ERR_* code otherwise; the message of
  * the calling thread's last failure is returned by mf_last_error().

@@ -5,22 +5,22 @@
 //              the workspace keeps -D and lse2 = lse * log2(e) per row.
 //   2. dq:     per 128-query tile (like the forward): recompute
 //              S^T = K Q^T and dP^T = V dO^T over the tile's non-empty key
-//              tiles, P^T = exp2(c S^T - lse2), dS^T = P^T (dP^T - D), and
-//              dQ^T += K^T dS^T.  K^T is staged k-permuted in LDS so dS^T is
-//              fed from its accumulator registers as the B operand.
+//              stages, P^T = exp2(c S^T - lse2), dS^T = P^T (dP^T - D), and
+//              dQ^T += K^T dS^T, with dS^T fed from its accumulator
+//              registers as the B operand and K^T read from the natural K
+//              tile in LDS by transposing reads.
 //   3. dkdv:   per 128-key tile and KV head: K and V stay in registers;
-//              for every non-empty query tile and every query head of the
+//              for every non-empty query stage and every query head of the
 //              GQA group, S = Q K^T and dP = dO V^T (accumulator column =
-//              key), then dV^T += dO^T P and dK^T += Q^T dS with Q^T and
-//              dO^T staged k-permuted in LDS.  The group's heads are summed
-//              in registers, which is the transpose of the reference's
-//              jnp.repeat of K/V (kernels/attention.py:19-22).
+//              key), then dV^T += dO^T P and dK^T += Q^T dS with dO^T and
+//              Q^T read transposed from the Q / dO tiles.  The group's heads
+//              are summed in registers, which is the transpose of the
+//              reference's jnp.repeat of K/V (kernels/attention.py:19-22).
+// The fp32 kernels (parity tests, smoke) stage through registers and read
+// single floats with v_mfma_f32_32x32x2_f32.
 // Rows with no valid key have lse = +inf, so their P is exactly 0 and they
 // contribute nothing; their dq is written as 0.
-#include <type_traits>
-
 #include "mf_common.h"
-#include "mf_kvstep.h"
 #include "mf_lds.h"
 
 namespace mf {
@@ -53,7 +53,6 @@ struct BwdArgs {
 };
 
 constexpr int kStep = 64;
-constexpr int kRow = kD + 8;   // bf16 LDS row pitch (144 B)
 constexpr int kRowF = kD + 1;  // fp32 LDS row pitch
 
 // ---------------------------------------------------------------------------
@@ -96,102 +95,52 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(BwdArgs a, int B) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. dq (per query tile)
+// 2. dq (per query tile), fp32
 // ---------------------------------------------------------------------------
-template <bool F32>
-struct DqLds;
-
-template <>
-struct DqLds<false> {
-  bf16 k[2][kStep * kRow];   // K   [key][d]
-  bf16 v[2][kStep * kRow];   // V   [key][d]
-  bf16 kt[2][kD * kRow];     // K^T [d][key, k-permuted]
-  int kid[2][kStep];
-};
-
-template <>
-struct DqLds<true> {
+struct DqLdsF32 {
   float k[2][kStep * kRowF];
   float v[2][kStep * kRowF];
   int kid[2][kStep];
 };
 
-template <bool F32>
-struct DqStage {
-  u32x4 r[F32 ? 8 : 4];
+struct StageF32 {
+  u32x4 r[8];
 };
 
-template <bool F32>
-__device__ __forceinline__ void dq_load(const BwdArgs& a, int b, int kvh, int kb, DqStage<F32>& st) {
+// K and V rows kb .. kb+63 of one KV head (zero past S) into registers.
+__device__ __forceinline__ void dq_load_f32(const BwdArgs& a, int b, int kvh, int kb, StageF32& st) {
   const int tid = threadIdx.x;
-  if constexpr (!F32) {
-    // threads 0..127: K, 4 consecutive keys x one d chunk (natural + transposed)
-    // threads 128..255: V, 4 consecutive keys x one d chunk (natural)
-    const bf16* src = reinterpret_cast<const bf16*>(tid < 128 ? a.k : a.v);
-    const int u = tid & 127;
-    const int kg = u >> 3, ch = u & 7;
+  const float* ks = reinterpret_cast<const float*>(a.k);
+  const float* vs = reinterpret_cast<const float*>(a.v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kb + kg * 4 + i;
-      st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
-                          : u32x4{0, 0, 0, 0};
-    }
-  } else {
-    const float* ks = reinterpret_cast<const float*>(a.k);
-    const float* vs = reinterpret_cast<const float*>(a.v);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + 256 * i;
-      const int key = kb + (u >> 4), ch = u & 15;
-      const size_t off = (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 4;
-      st.r[i] = key < a.S ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
-      st.r[4 + i] = key < a.S ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i;
+    const int key = kb + (u >> 4), ch = u & 15;
+    const size_t off = (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 4;
+    st.r[i] = key < a.S ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
+    st.r[4 + i] = key < a.S ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
   }
 }
 
-// Transposed store of 4 consecutive rows x 8 columns (bf16) into a
-// [col][row, k-permuted] LDS tile.
-__device__ __forceinline__ void store_transposed4x8(bf16* dst, int row0, int col0, const u32x4* r) {
-  const int pos = kperm_pos(row0);
-#pragma unroll
-  for (int dd = 0; dd < 8; ++dd) {
-    const int w = dd >> 1, sh = (dd & 1) * 16;
-    const uint32_t lo = ((r[0][w] >> sh) & 0xffffu) | (((r[1][w] >> sh) & 0xffffu) << 16);
-    const uint32_t hi = ((r[2][w] >> sh) & 0xffffu) | (((r[3][w] >> sh) & 0xffffu) << 16);
-    st_u32x2(dst + (col0 + dd) * kRow + pos, u32x2{lo, hi});
-  }
-}
-
-template <bool F32>
-__device__ __forceinline__ void dq_store(const BwdArgs& a, int b, int kb, const DqStage<F32>& st,
-                                         DqLds<F32>& lds, int buf) {
+__device__ __forceinline__ void dq_store_f32(const BwdArgs& a, int b, int kb, const StageF32& st,
+                                             DqLdsF32& lds, int buf) {
   const int tid = threadIdx.x;
   if (tid < kStep) lds.kid[buf][tid] = a.kid[(size_t)b * a.tk_pad + kb + tid];
-  if constexpr (!F32) {
-    const int u = tid & 127;
-    const int kg = u >> 3, ch = u & 7;
-    bf16* nat = tid < 128 ? lds.k[buf] : lds.v[buf];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st_u32x4(nat + (kg * 4 + i) * kRow + ch * 8, st.r[i]);
-    if (tid < 128) store_transposed4x8(lds.kt[buf], kg * 4, ch * 8, st.r);
-  } else {
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i;
+    const int key = u >> 4, ch = u & 15;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + 256 * i;
-      const int key = u >> 4, ch = u & 15;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lds.k[buf][key * kRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
-        lds.v[buf][key * kRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
-      }
+    for (int e = 0; e < 4; ++e) {
+      lds.k[buf][key * kRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
+      lds.v[buf][key * kRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
     }
   }
 }
 
-template <int HPW, bool F32>
-__global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
-  __shared__ DqLds<F32> lds;
+template <int HPW>
+__global__ __launch_bounds__(256) void bwd_dq_f32_kernel(BwdArgs a) {
+  __shared__ DqLdsF32 lds;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -211,37 +160,17 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int j = 0; j < HPW; ++j) head[j] = kvh * a.G + hc * HPW + j;
 
-  constexpr int kQRegs = F32 ? 32 : 4;
-  using QT = typename std::conditional<F32, float, bf16x8>::type;
-  QT qf[HPW][kQRegs], gf[HPW][kQRegs];
+  float qf[HPW][32], gf[HPW][32];
   float lse2[HPW], dlt[HPW];
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
     const size_t row = (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD;
-    if constexpr (!F32) {
-      const bf16* qs = reinterpret_cast<const bf16*>(a.q) + row + 8 * half;
-      const bf16* gs = reinterpret_cast<const bf16*>(a.dout) + row + 8 * half;
+    const float* qs = reinterpret_cast<const float*>(a.q) + row + half;
+    const float* gs = reinterpret_cast<const float*>(a.dout) + row + half;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (qvalid) {
-          qf[j][ks] = ld_bf16x8(qs + ks * 16);
-          gf[j][ks] = ld_bf16x8(gs + ks * 16);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            qf[j][ks][e] = (bf16)0.f;
-            gf[j][ks][e] = (bf16)0.f;
-          }
-        }
-      }
-    } else {
-      const float* qs = reinterpret_cast<const float*>(a.q) + row + half;
-      const float* gs = reinterpret_cast<const float*>(a.dout) + row + half;
-#pragma unroll
-      for (int st = 0; st < 32; ++st) {
-        qf[j][st] = qvalid ? qs[2 * st] : 0.f;
-        gf[j][st] = qvalid ? gs[2 * st] : 0.f;
-      }
+    for (int st = 0; st < 32; ++st) {
+      qf[j][st] = qvalid ? qs[2 * st] : 0.f;
+      gf[j][st] = qvalid ? gs[2 * st] : 0.f;
     }
     const size_t li = ((size_t)b * a.Hq + head[j]) * a.T + qpos;
     lse2[j] = qactive ? a.lse[li] * kLog2e : kPosInf;
@@ -260,11 +189,11 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
   const int nsteps = count;  // one 64-key stage per list entry
   const float c = a.scale_log2;
 
-  DqStage<F32> stage;
+  StageF32 stage;
   if (nsteps > 0) {
     const int kb0 = (list[0] >> 2) * kStep;
-    dq_load<F32>(a, b, kvh, kb0, stage);
-    dq_store<F32>(a, b, kb0, stage, lds, 0);
+    dq_load_f32(a, b, kvh, kb0, stage);
+    dq_store_f32(a, b, kb0, stage, lds, 0);
   }
   __syncthreads();
 
@@ -276,7 +205,7 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
     int next_kb = 0;
     if (step + 1 < nsteps) {
       next_kb = (list[step + 1] >> 2) * kStep;
-      dq_load<F32>(a, b, kvh, next_kb, stage);
+      dq_load_f32(a, b, kvh, next_kb, stage);
     }
 
 #pragma unroll
@@ -287,31 +216,16 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
         s[j] = zero16();
         dp[j] = zero16();
       }
-      if constexpr (!F32) {
-        const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kRow + 8 * half];
-        const bf16* vrow = &lds.v[buf][(kb2 * 32 + (lane & 31)) * kRow + 8 * half];
+      const float* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kRowF + half];
+      const float* vrow = &lds.v[buf][(kb2 * 32 + (lane & 31)) * kRowF + half];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 kf = ld_bf16x8(krow + ks * 16);
-          const bf16x8 vf = ld_bf16x8(vrow + ks * 16);
+      for (int st = 0; st < 32; ++st) {
+        const float kf = krow[2 * st];
+        const float vf = vrow[2 * st];
 #pragma unroll
-          for (int j = 0; j < HPW; ++j) {
-            s[j] = mfma32x32x16(kf, qf[j][ks], s[j]);
-            dp[j] = mfma32x32x16(vf, gf[j][ks], dp[j]);
-          }
-        }
-      } else {
-        const float* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kRowF + half];
-        const float* vrow = &lds.v[buf][(kb2 * 32 + (lane & 31)) * kRowF + half];
-#pragma unroll
-        for (int st = 0; st < 32; ++st) {
-          const float kf = krow[2 * st];
-          const float vf = vrow[2 * st];
-#pragma unroll
-          for (int j = 0; j < HPW; ++j) {
-            s[j] = mfma32x32x2(kf, qf[j][st], s[j]);
-            dp[j] = mfma32x32x2(vf, gf[j][st], dp[j]);
-          }
+        for (int j = 0; j < HPW; ++j) {
+          s[j] = mfma32x32x2(kf, qf[j][st], s[j]);
+          dp[j] = mfma32x32x2(vf, gf[j][st], dp[j]);
         }
       }
       // P^T and dS^T in place of s
@@ -336,83 +250,41 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(BwdArgs a) {
         }
       }
       // dQ^T += K^T dS^T
-      if constexpr (!F32) {
-        bf16x8 dsf[HPW][2];
 #pragma unroll
-        for (int j = 0; j < HPW; ++j) {
-          dsf[j][0] = pack8(s[j], 0);
-          dsf[j][1] = pack8(s[j], 8);
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float af = lds.k[buf][(kb2 * 32 + acc_row(r, lane)) * kRowF + db * 32 + (lane & 31)];
+#pragma unroll
+          for (int j = 0; j < HPW; ++j) dqacc[j][db] = mfma32x32x2(af, s[j][r], dqacc[j][db]);
         }
-#pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const bf16* ktrow = &lds.kt[buf][(db * 32 + (lane & 31)) * kRow + kb2 * 32 + 8 * half];
-#pragma unroll
-          for (int ks2 = 0; ks2 < 2; ++ks2) {
-            const bf16x8 af = ld_bf16x8(ktrow + ks2 * 16);
-#pragma unroll
-            for (int j = 0; j < HPW; ++j) dqacc[j][db] = mfma32x32x16(af, dsf[j][ks2], dqacc[j][db]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float af = lds.k[buf][(kb2 * 32 + acc_row(r, lane)) * kRowF + db * 32 + (lane & 31)];
-#pragma unroll
-            for (int j = 0; j < HPW; ++j) dqacc[j][db] = mfma32x32x2(af, s[j][r], dqacc[j][db]);
-          }
-      }
     }
 
-    if (step + 1 < nsteps) dq_store<F32>(a, b, next_kb, stage, lds, buf ^ 1);
+    if (step + 1 < nsteps) dq_store_f32(a, b, next_kb, stage, lds, buf ^ 1);
     __syncthreads();
   }
 
   if (!qvalid) return;
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
-    
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int d0 = db * 32 + 8 * g4 + 4 * half;
         const size_t off = (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + d0;
-        if constexpr (!F32) {
-          bf16x4 o;
+        f32x4 o;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = (bf16)(qactive ? dqacc[j][db][g4 * 4 + i] * a.scale : 0.f);
-          *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dq) + off) = o;
-        } else {
-          f32x4 o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = qactive ? dqacc[j][db][g4 * 4 + i] * a.scale : 0.f;
-          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dq) + off) = o;
-        }
+        for (int i = 0; i < 4; ++i) o[i] = qactive ? dqacc[j][db][g4 * 4 + i] * a.scale : 0.f;
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dq) + off) = o;
       }
   }
 }
 
 // ---------------------------------------------------------------------------
-// 3. dk, dv (per key tile and KV head)
+// 3. dk, dv (per key tile and KV head), fp32
 // ---------------------------------------------------------------------------
-template <bool F32>
-struct KvLds;
-
-template <>
-struct KvLds<false> {
-  bf16 q[2][kStep * kRow];    // Q    [query][d]
-  bf16 g[2][kStep * kRow];    // dO   [query][d]
-  bf16 qt[2][kD * kRow];      // Q^T  [d][query, k-permuted]
-  bf16 gt[2][kD * kRow];      // dO^T [d][query, k-permuted]
-  float lse2[2][kStep];
-  float dlt[2][kStep];
-  int qid[2][kStep];
-};
-
-template <>
-struct KvLds<true> {
+struct KvLdsF32 {
   float q[2][kStep * kRowF];
   float g[2][kStep * kRowF];
   float lse2[2][kStep];
@@ -420,9 +292,8 @@ struct KvLds<true> {
   int qid[2][kStep];
 };
 
-template <bool F32>
-struct KvStage {
-  u32x4 r[F32 ? 8 : 4];
+struct KvStageF32 {
+  u32x4 r[8];
   float lse2, dlt;
   int qid;
 };
@@ -436,31 +307,17 @@ __device__ __forceinline__ void kv_iter(const BwdArgs& a, const int* list, int i
   cls = entry & 3;
 }
 
-template <bool F32>
-__device__ __forceinline__ void kv_load(const BwdArgs& a, int b, int h, int qb, KvStage<F32>& st) {
+__device__ __forceinline__ void kv_load_f32(const BwdArgs& a, int b, int h, int qb, KvStageF32& st) {
   const int tid = threadIdx.x;
-  if constexpr (!F32) {
-    // thread -> (tensor, 4 consecutive queries, one d chunk)
-    const bf16* src = reinterpret_cast<const bf16*>((tid & 1) ? a.dout : a.q);
-    const int u = tid >> 1;
-    const int qg = u >> 3, ch = u & 7;
+  const float* qs = reinterpret_cast<const float*>(a.q);
+  const float* gs = reinterpret_cast<const float*>(a.dout);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int qq = qb + qg * 4 + i;
-      st.r[i] = qq < a.T ? ld_u32x4(src + (((size_t)b * a.T + qq) * a.Hq + h) * kD + ch * 8)
-                         : u32x4{0, 0, 0, 0};
-    }
-  } else {
-    const float* qs = reinterpret_cast<const float*>(a.q);
-    const float* gs = reinterpret_cast<const float*>(a.dout);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + 256 * i;
-      const int qq = qb + (u >> 4), ch = u & 15;
-      const size_t off = (((size_t)b * a.T + qq) * a.Hq + h) * kD + ch * 4;
-      st.r[i] = qq < a.T ? ld_u32x4(qs + off) : u32x4{0, 0, 0, 0};
-      st.r[4 + i] = qq < a.T ? ld_u32x4(gs + off) : u32x4{0, 0, 0, 0};
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i;
+    const int qq = qb + (u >> 4), ch = u & 15;
+    const size_t off = (((size_t)b * a.T + qq) * a.Hq + h) * kD + ch * 4;
+    st.r[i] = qq < a.T ? ld_u32x4(qs + off) : u32x4{0, 0, 0, 0};
+    st.r[4 + i] = qq < a.T ? ld_u32x4(gs + off) : u32x4{0, 0, 0, 0};
   }
   if (tid < kStep) {
     const int qq = qb + tid;
@@ -473,39 +330,27 @@ __device__ __forceinline__ void kv_load(const BwdArgs& a, int b, int h, int qb, 
   }
 }
 
-template <bool F32>
-__device__ __forceinline__ void kv_store(const KvStage<F32>& st, KvLds<F32>& lds, int buf) {
+__device__ __forceinline__ void kv_store_f32(const KvStageF32& st, KvLdsF32& lds, int buf) {
   const int tid = threadIdx.x;
   if (tid < kStep) {
     lds.qid[buf][tid] = st.qid;
     lds.lse2[buf][tid] = st.lse2;
     lds.dlt[buf][tid] = st.dlt;
   }
-  if constexpr (!F32) {
-    const int u = tid >> 1;
-    const int qg = u >> 3, ch = u & 7;
-    bf16* nat = (tid & 1) ? lds.g[buf] : lds.q[buf];
-    bf16* tr = (tid & 1) ? lds.gt[buf] : lds.qt[buf];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st_u32x4(nat + (qg * 4 + i) * kRow + ch * 8, st.r[i]);
-    store_transposed4x8(tr, qg * 4, ch * 8, st.r);
-  } else {
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i;
+    const int qq = u >> 4, ch = u & 15;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + 256 * i;
-      const int qq = u >> 4, ch = u & 15;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lds.q[buf][qq * kRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
-        lds.g[buf][qq * kRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
-      }
+    for (int e = 0; e < 4; ++e) {
+      lds.q[buf][qq * kRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
+      lds.g[buf][qq * kRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
     }
   }
 }
 
-template <bool F32>
-__global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
-  __shared__ KvLds<F32> lds;
+__global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(BwdArgs a) {
+  __shared__ KvLdsF32 lds;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -519,35 +364,15 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
   const bool kvalid = kpos < a.S;
 
   // K, V as B operands of S = Q K^T and dP = dO V^T
-  constexpr int kRegs = F32 ? 32 : 4;
-  using KT = typename std::conditional<F32, float, bf16x8>::type;
-  KT kf[kRegs], vf[kRegs];
+  float kf[32], vf[32];
   {
     const size_t row = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD;
-    if constexpr (!F32) {
-      const bf16* ks = reinterpret_cast<const bf16*>(a.k) + row + 8 * half;
-      const bf16* vs = reinterpret_cast<const bf16*>(a.v) + row + 8 * half;
+    const float* ks = reinterpret_cast<const float*>(a.k) + row + half;
+    const float* vs = reinterpret_cast<const float*>(a.v) + row + half;
 #pragma unroll
-      for (int ks2 = 0; ks2 < 4; ++ks2) {
-        if (kvalid) {
-          kf[ks2] = ld_bf16x8(ks + ks2 * 16);
-          vf[ks2] = ld_bf16x8(vs + ks2 * 16);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            kf[ks2][e] = (bf16)0.f;
-            vf[ks2][e] = (bf16)0.f;
-          }
-        }
-      }
-    } else {
-      const float* ks = reinterpret_cast<const float*>(a.k) + row + half;
-      const float* vs = reinterpret_cast<const float*>(a.v) + row + half;
-#pragma unroll
-      for (int st = 0; st < 32; ++st) {
-        kf[st] = kvalid ? ks[2 * st] : 0.f;
-        vf[st] = kvalid ? vs[2 * st] : 0.f;
-      }
+    for (int st = 0; st < 32; ++st) {
+      kf[st] = kvalid ? ks[2 * st] : 0.f;
+      vf[st] = kvalid ? vs[2 * st] : 0.f;
     }
   }
 
@@ -559,12 +384,12 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
   const int niters = count * a.G;  // (64-query stage, head) iterations
   const float c = a.scale_log2;
 
-  KvStage<F32> stage;
+  KvStageF32 stage;
   if (niters > 0) {
     int qb, hg, cls;
     kv_iter(a, list, 0, qb, hg, cls);
-    kv_load<F32>(a, b, kvh * a.G + hg, qb, stage);
-    kv_store<F32>(stage, lds, 0);
+    kv_load_f32(a, b, kvh * a.G + hg, qb, stage);
+    kv_store_f32(stage, lds, 0);
   }
   __syncthreads();
 
@@ -576,28 +401,18 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
     if (it + 1 < niters) {
       int qb2, hg2, cls2;
       kv_iter(a, list, it + 1, qb2, hg2, cls2);
-      kv_load<F32>(a, b, kvh * a.G + hg2, qb2, stage);
+      kv_load_f32(a, b, kvh * a.G + hg2, qb2, stage);
     }
 
 #pragma unroll
     for (int qb2 = 0; qb2 < 2; ++qb2) {
       f32x16 s = zero16(), dp = zero16();
-      if constexpr (!F32) {
-        const bf16* qrow = &lds.q[buf][(qb2 * 32 + (lane & 31)) * kRow + 8 * half];
-        const bf16* grow = &lds.g[buf][(qb2 * 32 + (lane & 31)) * kRow + 8 * half];
+      const float* qrow = &lds.q[buf][(qb2 * 32 + (lane & 31)) * kRowF + half];
+      const float* grow = &lds.g[buf][(qb2 * 32 + (lane & 31)) * kRowF + half];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          s = mfma32x32x16(ld_bf16x8(qrow + ks * 16), kf[ks], s);
-          dp = mfma32x32x16(ld_bf16x8(grow + ks * 16), vf[ks], dp);
-        }
-      } else {
-        const float* qrow = &lds.q[buf][(qb2 * 32 + (lane & 31)) * kRowF + half];
-        const float* grow = &lds.g[buf][(qb2 * 32 + (lane & 31)) * kRowF + half];
-#pragma unroll
-        for (int st = 0; st < 32; ++st) {
-          s = mfma32x32x2(qrow[2 * st], kf[st], s);
-          dp = mfma32x32x2(grow[2 * st], vf[st], dp);
-        }
+      for (int st = 0; st < 32; ++st) {
+        s = mfma32x32x2(qrow[2 * st], kf[st], s);
+        dp = mfma32x32x2(grow[2 * st], vf[st], dp);
       }
       // rows of s/dp are queries qq = qb2*32 + acc_row(r, lane); column = my key
 #pragma unroll
@@ -622,31 +437,17 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
           dp[r] = p * (dp[r] - dv4[i]);
         }
       }
-      if constexpr (!F32) {
-        const bf16x8 pf0 = pack8(s, 0), pf1 = pack8(s, 8);
-        const bf16x8 sf0 = pack8(dp, 0), sf1 = pack8(dp, 8);
 #pragma unroll
-        for (int db = 0; db < 2; ++db) {
-          const bf16* gtrow = &lds.gt[buf][(db * 32 + (lane & 31)) * kRow + qb2 * 32 + 8 * half];
-          const bf16* qtrow = &lds.qt[buf][(db * 32 + (lane & 31)) * kRow + qb2 * 32 + 8 * half];
-          dvacc[db] = mfma32x32x16(ld_bf16x8(gtrow), pf0, dvacc[db]);
-          dvacc[db] = mfma32x32x16(ld_bf16x8(gtrow + 16), pf1, dvacc[db]);
-          dkacc[db] = mfma32x32x16(ld_bf16x8(qtrow), sf0, dkacc[db]);
-          dkacc[db] = mfma32x32x16(ld_bf16x8(qtrow + 16), sf1, dkacc[db]);
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qq = qb2 * 32 + acc_row(r, lane);
+          dvacc[db] = mfma32x32x2(lds.g[buf][qq * kRowF + db * 32 + (lane & 31)], s[r], dvacc[db]);
+          dkacc[db] = mfma32x32x2(lds.q[buf][qq * kRowF + db * 32 + (lane & 31)], dp[r], dkacc[db]);
         }
-      } else {
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int qq = qb2 * 32 + acc_row(r, lane);
-            dvacc[db] = mfma32x32x2(lds.g[buf][qq * kRowF + db * 32 + (lane & 31)], s[r], dvacc[db]);
-            dkacc[db] = mfma32x32x2(lds.q[buf][qq * kRowF + db * 32 + (lane & 31)], dp[r], dkacc[db]);
-          }
-      }
     }
 
-    if (it + 1 < niters) kv_store<F32>(stage, lds, buf ^ 1);
+    if (it + 1 < niters) kv_store_f32(stage, lds, buf ^ 1);
     __syncthreads();
   }
 
@@ -658,25 +459,14 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(BwdArgs a) {
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d0 = db * 32 + 8 * g4 + 4 * half;
       const size_t off = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD + d0;
-      if constexpr (!F32) {
-        bf16x4 ok, ov;
+      f32x4 ok, ov;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ok[i] = (bf16)(kactive ? dkacc[db][g4 * 4 + i] * a.scale : 0.f);
-          ov[i] = (bf16)(kactive ? dvacc[db][g4 * 4 + i] : 0.f);
-        }
-        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dk) + off) = ok;
-        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dv) + off) = ov;
-      } else {
-        f32x4 ok, ov;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          ok[i] = kactive ? dkacc[db][g4 * 4 + i] * a.scale : 0.f;
-          ov[i] = kactive ? dvacc[db][g4 * 4 + i] : 0.f;
-        }
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dk) + off) = ok;
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dv) + off) = ov;
+      for (int i = 0; i < 4; ++i) {
+        ok[i] = kactive ? dkacc[db][g4 * 4 + i] * a.scale : 0.f;
+        ov[i] = kactive ? dvacc[db][g4 * 4 + i] : 0.f;
       }
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dk) + off) = ok;
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.dv) + off) = ov;
     }
 }
 
@@ -882,46 +672,40 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// bf16 dk/dv: 4*HS waves per workgroup for one 128-key tile of one KV head.
-// Waves w and w+4 own the same 32 keys (K, V as B operands in registers) and
-// process different query heads of the GQA group (slot w/4 takes heads
-// slot, slot+HS, ...), so each query step stages Q and dO of HS heads; their
-// dK/dV are summed through LDS at the end.  Q, dO, lse, D and the query ids
-// are DMA'd into a three-stage LDS ring of 64-query stages, two steps ahead
-// of use; dV^T += dO^T P and dK^T += Q^T dS read their transposed operands
-// from the Q / dO tiles.  Each 32-query block runs its scores, VALU and
-// accumulation before the next block starts: that keeps the kernel within
-// 168 VGPRs and 51 KB of LDS, i.e. three workgroups (12 waves) per CU, which
-// measured 10% faster at C2 and C3 than two workgroups with both blocks'
-// scores issued first and the two-slot ring of the forward.
+// bf16 dk/dv: 4 waves per workgroup for one 128-key tile of one KV head; each
+// wave owns 32 keys (K, V as B operands in registers) and walks the GQA
+// group's query heads in turn, summing their dK/dV in the same accumulators.
+// Q, dO, lse, D and the query ids are DMA'd into a three-stage LDS ring of
+// 64-query stages, two steps ahead of use; dV^T += dO^T P and dK^T += Q^T dS
+// read their transposed operands from the Q / dO tiles.  Each 32-query block
+// runs its scores, VALU and accumulation before the next block starts: that
+// keeps the kernel within 168 VGPRs and 51 KB of LDS, i.e. three workgroups
+// (12 waves) per CU, which measured 10% faster at C2 and C3 than two
+// workgroups with both blocks' scores issued first and the two-slot ring of
+// the forward.
 // ---------------------------------------------------------------------------
-template <int HS>
 struct QDma {
-  static constexpr int W = 4 * HS;
-  static constexpr int kTiles = 2 * HS;                      // Q, dO per slot
+  static constexpr int W = 4;
+  static constexpr int kTiles = 2;                           // Q, dO
   static constexpr int kGroupsPerWave = kTiles * 8 / W;      // 8-row groups
-  static constexpr int kWordArrays = 2 * HS + 1;             // lse, D per slot; ids
-  static_assert(kWordArrays <= W, "one word array per wave");
-  // stage layout: tiles [slot][Q, dO], then lse[slot][64], D[slot][64], ids[64]
+  static constexpr int kWordArrays = 3;                      // lse, D, ids
+  // stage layout: tiles [Q, dO], then lse[64], D[64], ids[64]
   static constexpr int kLseOff = kTiles * kTileBytes;
-  static constexpr int kDltOff = kLseOff + HS * 256;
-  static constexpr int kIdOff = kDltOff + HS * 256;
+  static constexpr int kDltOff = kLseOff + 256;
+  static constexpr int kIdOff = kDltOff + 256;
   static constexpr int kStageBytes = kIdOff + 256;
 };
 
-template <int HS>
-__global__ __launch_bounds__(256 * HS) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void bwd_dkdv_bf16_kernel(BwdArgs a) {
-  using Q = QDma<HS>;
+  using Q = QDma;
   constexpr int W = Q::W;
-  // two ring slots of 128 queries, each two 64-query stages
   __shared__ __attribute__((aligned(16))) char stage0[Q::kStageBytes], stage1[Q::kStageBytes],
       stage2[Q::kStageBytes];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = uniform(tid >> 6);
   const int half = lane >> 5;
-  const int slot = HS == 1 ? 0 : wave >> 2;
   // 1-D grid: (key-tile item in launch order, kvh), heads fastest
   const int kvh = uniform(blockIdx.x % a.Hkv);
   const int item = ld_const(a.korder, blockIdx.x / a.Hkv);  // (row, key tile), longest first
@@ -947,15 +731,14 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
 
   const int count = ld_const(a.kcnt, b * a.nk + kt);
   const int* list = a.klist + ((size_t)b * a.nk + kt) * 2 * a.nq;
-  const int hps = a.G / HS;        // heads per slot
+  const int hps = a.G;             // heads of the group, walked in turn
   const int niters = count * hps;  // (64-query stage, head) iterations
   const float c = a.scale_log2;
   const uint32_t qrow_stride = (uint32_t)a.Hq * kD * sizeof(bf16);
 
-  static_assert(W % 8 == 0 || 8 % W == 0, "8-row groups map to tiles statically");
   const char* const qbase = reinterpret_cast<const char*>(a.q);
   const char* const gbase = reinterpret_cast<const char*>(a.dout);
-  // DMA of iteration `it` (query rows qb .. qb+63 of HS heads) into a stage.
+  // DMA of iteration `it` (query rows qb .. qb+63 of one head) into a stage.
   auto issue = [&](int it, char* stage) {
     it = min(it, niters - 1);
     const int entry = ld_const(list, it / hps);
@@ -965,25 +748,23 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     if (wave < Q::kWordArrays) {
       // rows past T re-read row T-1 (finite values); their ids are 0, so
       // every pair they form is masked or belongs to a zeroed inactive key
-      const int s = min(wave >> 1, HS - 1);
-      const size_t row = ((size_t)b * a.Hq + kvh * a.G + s + HS * hj) * a.T;
-      const void* sbase = wave == 2 * HS ? (const void*)(a.qid + (size_t)b * a.tq_pad + qb)
-                          : (wave & 1)   ? (const void*)(a.ndelta + row)
-                                         : (const void*)(a.lse2 + row);
-      const uint32_t voff = 4u * (wave == 2 * HS ? lane : min(qb + lane, a.T - 1));
-      char* dst = wave == 2 * HS ? stage + Q::kIdOff
-                  : (wave & 1)   ? stage + Q::kDltOff + s * 256
-                                 : stage + Q::kLseOff + s * 256;
+      const size_t row = ((size_t)b * a.Hq + kvh * a.G + hj) * a.T;
+      const void* sbase = wave == 2 ? (const void*)(a.qid + (size_t)b * a.tq_pad + qb)
+                          : (wave & 1) ? (const void*)(a.ndelta + row)
+                                       : (const void*)(a.lse2 + row);
+      const uint32_t voff = 4u * (wave == 2 ? lane : min(qb + lane, a.T - 1));
+      char* dst = wave == 2 ? stage + Q::kIdOff
+                  : (wave & 1) ? stage + Q::kDltOff
+                               : stage + Q::kLseOff;
       dma_word64(sbase, voff, dst);
     }
 #pragma unroll
     for (int j = 0; j < Q::kGroupsPerWave; ++j) {
-      // 8-row group wave + W j: with wave < W and W a divisor or multiple of
-      // 8, its tile (W j) / 8 is a compile-time constant, so the Q / dO
-      // choice is a register select rather than a reload of the argument
+      // 8-row group wave + W j: its tile (W j) / 8 is a compile-time
+      // constant, so the Q / dO choice is a register select rather than a
+      // reload of the argument
       const int tile = (W * j) >> 3, r0 = 8 * ((wave + W * j) & 7);
-      const int s = tile >> 1;                 // head slot of this tile
-      const int h = kvh * a.G + s + HS * hj;
+      const int h = kvh * a.G + hj;
       const char* base = ((tile & 1) ? gbase : qbase) + ((size_t)b * a.T * a.Hq + h) * kD * sizeof(bf16);
       dma_rows8(base, qrow_stride, qb, r0, a.T - 1, stage + tile * kTileBytes);
     }
@@ -1075,10 +856,10 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     const int entry = ld_const(list, it / hps);
     const int qb = (entry >> 2) * kKvStep;
     const bool partial = (entry & 3) == 1;
-    const char* qt = stage + 2 * slot * kTileBytes;
-    const char* gt = stage + (2 * slot + 1) * kTileBytes;
-    const float* lse_l = reinterpret_cast<const float*>(stage + Q::kLseOff + slot * 256);
-    const float* ndlt_l = reinterpret_cast<const float*>(stage + Q::kDltOff + slot * 256);
+    const char* qt = stage;
+    const char* gt = stage + kTileBytes;
+    const float* lse_l = reinterpret_cast<const float*>(stage + Q::kLseOff);
+    const float* ndlt_l = reinterpret_cast<const float*>(stage + Q::kDltOff);
     const int* qid_l = reinterpret_cast<const int*>(stage + Q::kIdOff);
     bool run[2] = {true, true}, mask_ids[2] = {false, false}, diag[2] = {false, false};
     if (partial) {
@@ -1138,32 +919,6 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   }
   wait_vmcnt<0>();
 
-  if constexpr (HS == 2) {
-    // slot 1 hands its partial dK (through ring slot A) and dV (through B)
-    // to slot 0; the ring is idle once every wave has passed the barrier
-    static_assert(4 * 64 * 32 * sizeof(float) <= Q::kStageBytes, "reduction buffer");
-    barrier();
-    float* kred = reinterpret_cast<float*>(stage0) + ((wave & 3) * 64 + lane) * 32;
-    float* vred = reinterpret_cast<float*>(stage1) + ((wave & 3) * 64 + lane) * 32;
-    if (slot == 1) {
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          kred[db * 16 + r] = dkacc[db][r];
-          vred[db * 16 + r] = dvacc[db][r];
-        }
-    }
-    __syncthreads();
-    if (slot == 1) return;
-#pragma unroll
-    for (int db = 0; db < 2; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        dkacc[db][r] += kred[db * 16 + r];
-        dvacc[db][r] += vred[db * 16 + r];
-      }
-  }
   if (!kvalid) return;
   const bool kactive = mykid != 0;
 #pragma unroll
@@ -1239,9 +994,9 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   if (!(phases & 2)) {
   } else if (f32) {
     if (hpw == 2)
-      hipLaunchKernelGGL((bwd_dq_kernel<2, true>), qgrid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dq_f32_kernel<2>), qgrid, dim3(256), 0, stream, a);
     else
-      hipLaunchKernelGGL((bwd_dq_kernel<1, true>), qgrid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dq_f32_kernel<1>), qgrid, dim3(256), 0, stream, a);
   } else {
     if (hpw == 2)
       hipLaunchKernelGGL((bwd_dq_bf16_kernel<2>), qgrid, dim3(512), 0, stream, a);
@@ -1250,13 +1005,13 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   }
   const dim3 kgrid(Hkv * batch * lay.nk);
   if (phases & 4) {
-    // One head slot (4-wave workgroups, two per CU): measured 11-32% faster
-    // than two slots in one 8-wave workgroup at C2/C3/C5, because the two
-    // workgroups of a CU do not share barriers.
+    // 4-wave workgroups, one head at a time: measured 11-32% faster at
+    // C2/C3/C5 than 8-wave workgroups whose halves took different heads and
+    // summed through LDS, because the workgroups of a CU share no barriers.
     if (f32)
-      hipLaunchKernelGGL((bwd_dkdv_kernel<true>), kgrid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL(bwd_dkdv_f32_kernel, kgrid, dim3(256), 0, stream, a);
     else
-      hipLaunchKernelGGL((bwd_dkdv_bf16_kernel<1>), kgrid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL(bwd_dkdv_bf16_kernel, kgrid, dim3(256), 0, stream, a);
   }
   return hipGetLastError();
 }

@@ -1,12 +1,12 @@
 // Flash-style forward for segment-masked GQA attention on gfx950.
 //
 // Two kernels: the bf16 one (further below; the benchmarked path) and an
-// fp32 template.  fp32 work unit: one workgroup = 4 waves = one 128-query
+// fp32 one.  fp32 work unit: one workgroup = 4 waves = one 128-query
 // tile of one row, for HPW (1 or 2) query heads that share a KV head.  Each
 // wave owns 32 queries for all HPW heads, so every K / V^T fragment it reads
 // from LDS feeds HPW MFMAs (the GQA sharing of K/V tiles).  The workgroup
 // walks the compacted list of non-empty 128-key tiles of its query tile (from
-// the block map) in 64-key steps, double-buffering K and V^T in LDS.
+// the block map) in 64-key steps, double-buffering K and V in LDS.
 //
 // Scores are formed transposed, S^T = K Q^T, so an accumulator column is one
 // query: the row max and row sum are in-lane reductions plus one
@@ -14,10 +14,7 @@
 // layout of the B operand of O^T += V^T P^T.  PARTIAL tiles compare the
 // canonical ids (and causality) per element; FULL tiles skip the compare.
 // Online softmax in base 2 with the logit scale folded into one FMA.
-#include <type_traits>
-
 #include "mf_common.h"
-#include "mf_kvstep.h"
 #include "mf_lds.h"
 
 namespace mf {
@@ -46,112 +43,53 @@ struct FwdArgs {
 };
 
 constexpr int kStepK = 64;          // keys per inner step
-constexpr int kLdsRow = kD + 8;     // bf16 row pitch (144 B): conflict-free b128 reads
-constexpr int kLdsRowF = kD + 1;    // fp32 row pitch (65 floats)
+constexpr int kLdsRowF = kD + 1;    // fp32 LDS row pitch (65 floats)
 
-template <bool F32>
-struct FwdLds;
-
-template <>
-struct FwdLds<false> {
-  bf16 k[2][kStepK * kLdsRow];   // K    [key][d]
-  bf16 vt[2][kD * kLdsRow];      // V^T  [d][key, k-permuted]
-  int kid[2][kStepK];
-};
-
-template <>
-struct FwdLds<true> {
+struct FwdLdsF32 {
   float k[2][kStepK * kLdsRowF];  // K [key][d]
   float v[2][kStepK * kLdsRowF];  // V [key][d]
   int kid[2][kStepK];
 };
 
 // Global -> register staging of one 64-key step (K and V) for the workgroup.
-template <bool F32>
-struct FwdStage {
-  u32x4 r[F32 ? 8 : 4];
+struct FwdStageF32 {
+  u32x4 r[8];
 };
 
-template <bool F32>
-__device__ __forceinline__ void fwd_load(const FwdArgs& a, int b, int kvh, int kb,
-                                         FwdStage<F32>& st) {
+__device__ __forceinline__ void fwd_load_f32(const FwdArgs& a, int b, int kvh, int kb,
+                                             FwdStageF32& st) {
   const int tid = threadIdx.x;
-  if constexpr (!F32) {
-    const bf16* src = reinterpret_cast<const bf16*>(tid < 128 ? a.v : a.k);
-    if (tid < 128) {
-      // V: 4 consecutive keys x one 8-wide d chunk per thread
-      const int kg = tid >> 3, ch = tid & 7;
+  const float* ks = reinterpret_cast<const float*>(a.k);
+  const float* vs = reinterpret_cast<const float*>(a.v);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kb + kg * 4 + i;
-        st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
-                            : u32x4{0, 0, 0, 0};
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int u = (tid - 128) + 128 * i;
-        const int key = kb + (u >> 3), ch = u & 7;
-        st.r[i] = key < a.S ? ld_u32x4(src + (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 8)
-                            : u32x4{0, 0, 0, 0};
-      }
-    }
-  } else {
-    const float* ks = reinterpret_cast<const float*>(a.k);
-    const float* vs = reinterpret_cast<const float*>(a.v);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + 256 * i;
-      const int key = kb + (u >> 4), ch = u & 15;
-      const size_t off = (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 4;
-      st.r[i] = key < a.S ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
-      st.r[4 + i] = key < a.S ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i;
+    const int key = kb + (u >> 4), ch = u & 15;
+    const size_t off = (((size_t)b * a.S + key) * a.Hkv + kvh) * kD + ch * 4;
+    st.r[i] = key < a.S ? ld_u32x4(ks + off) : u32x4{0, 0, 0, 0};
+    st.r[4 + i] = key < a.S ? ld_u32x4(vs + off) : u32x4{0, 0, 0, 0};
   }
 }
 
-template <bool F32>
-__device__ __forceinline__ void fwd_store(const FwdArgs& a, int b, int kb, const FwdStage<F32>& st,
-                                          FwdLds<F32>& lds, int buf) {
+__device__ __forceinline__ void fwd_store_f32(const FwdArgs& a, int b, int kb,
+                                              const FwdStageF32& st, FwdLdsF32& lds, int buf) {
   const int tid = threadIdx.x;
   if (tid < kStepK) lds.kid[buf][tid] = a.kid[(size_t)b * a.tk_pad + kb + tid];
-  if constexpr (!F32) {
-    if (tid < 128) {
-      const int kg = tid >> 3, ch = tid & 7;
-      const int pos = kperm_pos(kg * 4);
 #pragma unroll
-      for (int dd = 0; dd < 8; ++dd) {
-        // element dd of each key's 8-wide chunk: 16-bit lane dd of the u32x4
-        uint32_t lo = 0, hi = 0;
-        const int w = dd >> 1, sh = (dd & 1) * 16;
-        lo = ((st.r[0][w] >> sh) & 0xffffu) | (((st.r[1][w] >> sh) & 0xffffu) << 16);
-        hi = ((st.r[2][w] >> sh) & 0xffffu) | (((st.r[3][w] >> sh) & 0xffffu) << 16);
-        st_u32x2(&lds.vt[buf][(ch * 8 + dd) * kLdsRow + pos], u32x2{lo, hi});
-      }
-    } else {
+  for (int i = 0; i < 4; ++i) {
+    const int u = tid + 256 * i;
+    const int key = u >> 4, ch = u & 15;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int u = (tid - 128) + 128 * i;
-        st_u32x4(&lds.k[buf][(u >> 3) * kLdsRow + (u & 7) * 8], st.r[i]);
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = tid + 256 * i;
-      const int key = u >> 4, ch = u & 15;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        lds.k[buf][key * kLdsRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
-        lds.v[buf][key * kLdsRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
-      }
+    for (int e = 0; e < 4; ++e) {
+      lds.k[buf][key * kLdsRowF + ch * 4 + e] = __uint_as_float(st.r[i][e]);
+      lds.v[buf][key * kLdsRowF + ch * 4 + e] = __uint_as_float(st.r[4 + i][e]);
     }
   }
 }
 
-template <int HPW, bool F32>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
-  __shared__ FwdLds<F32> lds;
+template <int HPW>
+__global__ __launch_bounds__(256) void attn_fwd_f32_kernel(FwdArgs a) {
+  __shared__ FwdLdsF32 lds;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
@@ -171,29 +109,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
   for (int j = 0; j < HPW; ++j) head[j] = kvh * a.G + hc * HPW + j;
 
   // ---- query fragments (B operand of S^T = K Q^T) -----------------------
-  constexpr int kQRegs = F32 ? 32 : 4;
-  using QT = typename std::conditional<F32, float, bf16x8>::type;
-  QT qf[HPW][kQRegs];
+  float qf[HPW][32];
 #pragma unroll
   for (int j = 0; j < HPW; ++j) {
-    if constexpr (!F32) {
-      const bf16* src = reinterpret_cast<const bf16*>(a.q) +
-                        (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + 8 * half;
+    const float* src = reinterpret_cast<const float*>(a.q) +
+                       (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + half;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (qvalid) {
-          qf[j][ks] = ld_bf16x8(src + ks * 16);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) qf[j][ks][e] = (bf16)0.f;
-        }
-      }
-    } else {
-      const float* src = reinterpret_cast<const float*>(a.q) +
-                         (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + half;
-#pragma unroll
-      for (int st = 0; st < 32; ++st) qf[j][st] = qvalid ? src[2 * st] : 0.f;
-    }
+    for (int st = 0; st < 32; ++st) qf[j][st] = qvalid ? src[2 * st] : 0.f;
   }
 
   f32x16 oacc[HPW][2];
@@ -211,11 +133,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
   const int nsteps = count;  // one 64-key stage per list entry
   const float c = a.scale_log2;
 
-  FwdStage<F32> stage;
+  FwdStageF32 stage;
   if (nsteps > 0) {
     const int e0 = list[0];
-    fwd_load<F32>(a, b, kvh, (e0 >> 2) * kStepK, stage);
-    fwd_store<F32>(a, b, (e0 >> 2) * kStepK, stage, lds, 0);
+    fwd_load_f32(a, b, kvh, (e0 >> 2) * kStepK, stage);
+    fwd_store_f32(a, b, (e0 >> 2) * kStepK, stage, lds, 0);
   }
   __syncthreads();
 
@@ -227,7 +149,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     int next_kb = 0;
     if (step + 1 < nsteps) {
       next_kb = (list[step + 1] >> 2) * kStepK;
-      fwd_load<F32>(a, b, kvh, next_kb, stage);
+      fwd_load_f32(a, b, kvh, next_kb, stage);
     }
 
     // ---- S^T = K Q^T for two 32-key blocks --------------------------------
@@ -236,22 +158,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
       for (int j = 0; j < HPW; ++j) s[j][kb2] = zero16();
-      if constexpr (!F32) {
-        const bf16* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kLdsRow + 8 * half];
+      const float* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kLdsRowF + half];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 af = ld_bf16x8(krow + ks * 16);
+      for (int st = 0; st < 32; ++st) {
+        const float af = krow[2 * st];
 #pragma unroll
-          for (int j = 0; j < HPW; ++j) s[j][kb2] = mfma32x32x16(af, qf[j][ks], s[j][kb2]);
-        }
-      } else {
-        const float* krow = &lds.k[buf][(kb2 * 32 + (lane & 31)) * kLdsRowF + half];
-#pragma unroll
-        for (int st = 0; st < 32; ++st) {
-          const float af = krow[2 * st];
-#pragma unroll
-          for (int j = 0; j < HPW; ++j) s[j][kb2] = mfma32x32x2(af, qf[j][st], s[j][kb2]);
-        }
+        for (int j = 0; j < HPW; ++j) s[j][kb2] = mfma32x32x2(af, qf[j][st], s[j][kb2]);
       }
     }
 
@@ -306,41 +218,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
     }
 
     // ---- O^T += V^T P^T -------------------------------------------------------
-    if constexpr (!F32) {
-      bf16x8 pf[HPW][2][2];
 #pragma unroll
-      for (int j = 0; j < HPW; ++j)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
-          pf[j][kb2][0] = pack8(s[j][kb2], 0);
-          pf[j][kb2][1] = pack8(s[j][kb2], 8);
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float vf = lds.v[buf][(kb2 * 32 + acc_row(r, lane)) * kLdsRowF + db * 32 + (lane & 31)];
+#pragma unroll
+          for (int j = 0; j < HPW; ++j) oacc[j][db] = mfma32x32x2(vf, s[j][kb2][r], oacc[j][db]);
         }
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const bf16* vrow = &lds.vt[buf][(db * 32 + (lane & 31)) * kLdsRow + 8 * half];
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-          for (int ks2 = 0; ks2 < 2; ++ks2) {
-            const bf16x8 vf = ld_bf16x8(vrow + kb2 * 32 + ks2 * 16);
-#pragma unroll
-            for (int j = 0; j < HPW; ++j) oacc[j][db] = mfma32x32x16(vf, pf[j][kb2][ks2], oacc[j][db]);
-          }
-      }
-    } else {
-#pragma unroll
-      for (int db = 0; db < 2; ++db)
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float vf = lds.v[buf][(kb2 * 32 + acc_row(r, lane)) * kLdsRowF + db * 32 + (lane & 31)];
-#pragma unroll
-            for (int j = 0; j < HPW; ++j) oacc[j][db] = mfma32x32x2(vf, s[j][kb2][r], oacc[j][db]);
-          }
-    }
 
-    if (step + 1 < nsteps) fwd_store<F32>(a, b, next_kb, stage, lds, buf ^ 1);
+    if (step + 1 < nsteps) fwd_store_f32(a, b, next_kb, stage, lds, buf ^ 1);
     __syncthreads();
   }
 
@@ -361,17 +250,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(FwdArgs a) {
         for (int g4 = 0; g4 < 4; ++g4) {
           const int d0 = db * 32 + 8 * g4 + 4 * half;
           const size_t off = (((size_t)b * a.T + qpos) * a.Hq + head[j]) * kD + d0;
-          if constexpr (!F32) {
-            bf16x4 o;
+          f32x4 o;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = (bf16)(has ? oacc[j][db][g4 * 4 + i] * inv : 0.f);
-            *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.out) + off) = o;
-          } else {
-            f32x4 o;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] = has ? oacc[j][db][g4 * 4 + i] * inv : 0.f;
-            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + off) = o;
-          }
+          for (int i = 0; i < 4; ++i) o[i] = has ? oacc[j][db][g4 * 4 + i] * inv : 0.f;
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + off) = o;
         }
     }
   }
@@ -753,9 +635,9 @@ hipError_t launch_attn_fwd(const void* q, const void* k, const void* v, bool f32
   const dim3 grid(Hkv * a.hchunks * batch * a.nq);
   if (f32) {
     if (hpw == 2)
-      hipLaunchKernelGGL((attn_fwd_kernel<2, true>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<2>), grid, dim3(256), 0, stream, a);
     else
-      hipLaunchKernelGGL((attn_fwd_kernel<1, true>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<1>), grid, dim3(256), 0, stream, a);
   } else {
     if (hpw == 2)
       hipLaunchKernelGGL((attn_fwd_bf16_kernel<2, false>), grid, dim3(512), 0, stream, a);

@@ -9,7 +9,8 @@
 //       B[k = l/32][n = l%32] (one float each).
 // A contraction may visit its k indices in any order as long as A and B
 // agree; the kernels use that freedom to feed accumulator registers straight
-// back in as B operands (see acc_row / kperm_pos below).
+// back in as B operands (acc_row below gives the rows a lane holds), paired
+// with transposing LDS reads of the other operand that visit the same rows.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -36,17 +37,6 @@ constexpr float kPosInf = __builtin_huge_valf();
 // Row (within a 32-row accumulator block) held by register r of lane l.
 __device__ __forceinline__ int acc_row(int r, int lane) {
   return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-}
-
-// Position of key (or query) index kk (0..63 within a 64-block) in the
-// "k-permuted" LDS layout used for transposed operands.  Inside every group
-// of 16, the 4-element runs are stored in the order 0,2,1,3 so that the 8
-// values lane half h needs for one MFMA k-step -- accumulator rows
-// {0-3, 8-11} (h = 0) or {4-7, 12-15} (h = 1) -- are 8 contiguous slots.
-__device__ __forceinline__ int kperm_pos(int kk) {
-  const int g = (kk >> 2) & 3;                 // 4-run inside the 16-group
-  const int slot = (g == 1) ? 2 : (g == 2) ? 1 : g;
-  return (kk & ~15) | (slot << 2) | (kk & 3);
 }
 
 __device__ __forceinline__ f32x16 mfma32x32x16(const bf16x8& a, const bf16x8& b,
@@ -132,10 +122,6 @@ __device__ __forceinline__ u32x4 ld_u32x4(const void* p) {
 
 __device__ __forceinline__ void st_u32x4(void* p, const u32x4& v) {
   *reinterpret_cast<u32x4*>(p) = v;
-}
-
-__device__ __forceinline__ void st_u32x2(void* p, const u32x2& v) {
-  *reinterpret_cast<u32x2*>(p) = v;
 }
 
 // A wave-uniform integer forced into a scalar register.  Index arithmetic

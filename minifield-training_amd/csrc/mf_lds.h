@@ -103,6 +103,14 @@ __device__ __forceinline__ bf16x8 tile_tr_operand(const char* tile, int row, int
   return __builtin_bit_cast(bf16x8, w);
 }
 
+constexpr int kKvStep = 64;  // rows per ring stage (keys, or queries in dk/dv)
+
+// Lane addressing of the transposing reads that build a [d][row] operand
+// from a natural [row][d] tile: add (block base + tr_row) rows and
+// (32 * d block + tr_col) columns; the second read of a k-step is 8 rows on.
+__device__ __forceinline__ int tr_row_of(int lane) { return ((lane & 15) >> 2) + 4 * (lane >> 5); }
+__device__ __forceinline__ int tr_col_of(int lane) { return 16 * ((lane >> 4) & 1) + 4 * (lane & 3); }
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt immediate out of range");

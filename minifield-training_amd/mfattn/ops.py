@@ -66,6 +66,31 @@ def _require_shape(t: torch.Tensor, shape: tuple[int, ...], what: str) -> None:
         raise ValueError(f"{what} must be {list(shape)}, got {list(t.shape)}")
 
 
+def require_contiguous(what: str, *tensors: torch.Tensor) -> None:
+    """The kernels address every operand as a dense row-major array from its
+    ``data_ptr()``: a slice or transposed view would be read (or written) as
+    if it were dense, so it is refused before any launch.  Callers that hold
+    views pass ``.contiguous()`` copies (the drop-in functions do)."""
+    for t in tensors:
+        if t is not None and not t.is_contiguous():
+            raise ValueError(f"{what} must be contiguous (got a strided view of shape "
+                             f"{list(t.shape)}); pass .contiguous()")
+
+
+def _require_lse(lse: torch.Tensor, b: int, hq: int, t: int) -> None:
+    if lse.dtype != torch.float32:
+        raise ValueError("lse must be float32")
+    _require_shape(lse, (b, hq, t), "lse")
+    require_contiguous("lse", lse)
+
+
+def _require_workspace(ws: torch.Tensor, b: int, t: int, hq: int) -> None:
+    need = _lib.LIB.mf_attn_bwd_workspace_bytes(b, t, hq)
+    if ws.dtype != torch.uint8 or ws.numel() < need:
+        raise ValueError(f"the backward workspace must be a uint8 tensor of at least {need} bytes")
+    require_contiguous("the backward workspace", ws)
+
+
 def as_mask(mask: torch.Tensor, mode: int) -> tuple[torch.Tensor, int]:
     """Mask in a dtype the C ABI reads (int32 or uint8), values preserved.
 
@@ -164,6 +189,7 @@ def check_attention_operands(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape or q.shape[0] != k.shape[0] \
             or q.shape[3] != k.shape[3]:
         raise ValueError("Packed attention query/KV shapes are incompatible")
+    require_contiguous("query, key and value", q, k, v)
     if plan is not None:
         if (plan.batch, plan.q_len, plan.kv_len) != (q.shape[0], q.shape[1], k.shape[1]):
             raise ValueError(
@@ -208,6 +234,7 @@ def attn_fwd_rope_q(q_raw: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("q_gain must be a [D] tensor of the query's dtype")
     if positions is not None and (positions.shape != (b, t) or positions.dtype != torch.int32):
         raise ValueError("positions must be a [B, T] int32 tensor")
+    require_contiguous("positions", positions)
     q_gain = q_gain.contiguous()
     table_bytes = _lib.LIB.mf_rope_table_bytes(b, t)
     table = torch.empty(table_bytes // 4, dtype=torch.int32, device=device)
@@ -225,9 +252,11 @@ def attn_bwd(q, k, v, out, dout, lse, plan: Plan, mode: int, scale: float):
     code = same_dtype("query, key, value, output and its gradient", q, k, v, out, dout)
     if out.shape != q.shape or dout.shape != q.shape:
         raise ValueError("the output and its gradient must have the query's shape")
-    device = require_device(q, k, v, out, dout, lse)
+    require_contiguous("the output and its gradient", out, dout)
     b, t, hq, d = q.shape
     s, hkv = k.shape[1], k.shape[2]
+    _require_lse(lse, b, hq, t)
+    device = require_device(q, k, v, out, dout, lse)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
@@ -249,7 +278,12 @@ def bwd_workspace(q: torch.Tensor) -> torch.Tensor:
 def attn_bwd_delta(out, dout, lse, ws) -> None:
     """Phase 1 of the backward: -rowsum(dO * O) and lse * log2(e) into ``ws``."""
     same_dtype("output and its gradient", out, dout)
+    if dout.shape != out.shape or out.dim() != 4:
+        raise ValueError("the output and its gradient must be [B, T, Hq, D] of one shape")
+    require_contiguous("the output and its gradient", out, dout)
     b, t, hq, d = out.shape
+    _require_lse(lse, b, hq, t)
+    _require_workspace(ws, b, t, hq)
     _lib.check(_lib.LIB.mf_attn_bwd_delta(_ptr(out), _ptr(dout), _ptr(lse), dtype_code(out), b, t,
                                           hq, d, _ptr(ws), ws.numel(), _stream(out.device)))
 
@@ -258,8 +292,13 @@ def attn_bwd_dq(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, dq)
     """Phase 2 of the backward: dq (reads the delta phase's ``ws``)."""
     check_attention_operands(q, k, v, plan, mode)
     same_dtype("query, output gradient and dq", q, dout, dq)
+    if dout.shape != q.shape or dq.shape != q.shape:
+        raise ValueError("the output gradient and dq must have the query's shape")
+    require_contiguous("the output gradient and dq", dout, dq)
     b, t, hq, d = q.shape
     s, hkv = k.shape[1], k.shape[2]
+    _require_lse(lse, b, hq, t)
+    _require_workspace(ws, b, t, hq)
     _lib.check(_lib.LIB.mf_attn_bwd_dq(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse),
                                        dtype_code(q), b, t, s, hq, hkv, d, mode, float(scale),
                                        _ptr(plan.buf), plan.nbytes, _ptr(dq), _ptr(ws), ws.numel(),
@@ -270,8 +309,13 @@ def attn_bwd_dkdv(q, k, v, dout, lse, plan: Plan, mode: int, scale: float, ws, d
     """Phase 3 of the backward: dk and dv (reads the delta phase's ``ws``)."""
     check_attention_operands(q, k, v, plan, mode)
     same_dtype("query, output gradient, dk and dv", q, dout, dk, dv)
+    if dout.shape != q.shape or dk.shape != k.shape or dv.shape != k.shape:
+        raise ValueError("the output gradient must have the query's shape, dk and dv the key's")
+    require_contiguous("the output gradient, dk and dv", dout, dk, dv)
     b, t, hq, d = q.shape
     s, hkv = k.shape[1], k.shape[2]
+    _require_lse(lse, b, hq, t)
+    _require_workspace(ws, b, t, hq)
     _lib.check(_lib.LIB.mf_attn_bwd_dkdv(_ptr(q), _ptr(k), _ptr(v), _ptr(dout), _ptr(lse),
                                          dtype_code(q), b, t, s, hq, hkv, d, mode, float(scale),
                                          _ptr(plan.buf), plan.nbytes, _ptr(dk), _ptr(dv), _ptr(ws),
@@ -347,6 +391,17 @@ class PlanCache:
     modified tensor misses.  Writes that bypass torch (a raw pointer handed to
     other code) are not seen: such callers pass ``plan=`` explicitly or clear
     the cache.
+
+    Two cases never touch the cache:
+
+    * graph capture: a captured step must record its own block map, because
+      a replay runs with whatever ids the static input buffers then hold
+      (copied in with ``copy_`` between replays), and a plan built under
+      capture holds nothing until the graph is replayed, so it is neither
+      looked up nor stored while the current stream is capturing;
+    * another stream: the key includes the current stream, so a plan is only
+      reused on the stream that built it, where stream order already makes
+      its contents visible to every later call.
     """
 
     def __init__(self, capacity: int = 8):
@@ -361,9 +416,11 @@ class PlanCache:
 
     def get(self, segment_ids: torch.Tensor | None, mask: torch.Tensor, mode: int, q_len: int,
             kv_len: int, batch: int) -> Plan:
-        if not self.enabled:
+        if not self.enabled or (mask.device.type == "cuda"
+                                and torch.cuda.is_current_stream_capturing()):
             return block_map(segment_ids, mask, mode, q_len, kv_len, batch)
-        key = (id(segment_ids), id(mask), mode, q_len, kv_len, batch, mask.device)
+        stream = _stream(mask.device) if mask.device.type == "cuda" else None
+        key = (id(segment_ids), id(mask), mode, q_len, kv_len, batch, mask.device, stream)
         with self._lock:
             entry = self._entries.get(key)
             if entry is not None:

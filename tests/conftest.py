@@ -40,3 +40,16 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
     return torch.device("cuda:0")
+
+
+def pytest_terminal_summary(terminalreporter):
+    """One line per full-shape bf16 parity case (C2-C5 outputs and gradients): the raw
+    max-abs error against the fp32 reference and the error beyond one bf16 rounding,
+    which the tests hold below 2e-2."""
+    helpers = sys.modules.get("_helpers")
+    rows = getattr(helpers, "PARITY_SUMMARY", None) if helpers else None
+    if not rows:
+        return
+    terminalreporter.write_sep("-", "bf16 parity at the BASELINE shapes")
+    for label, raw, excess in rows:
+        terminalreporter.write_line(f"{label:<10} max-abs {raw:.4f}  beyond-rounding {excess:.4f}")

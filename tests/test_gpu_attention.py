@@ -572,7 +572,7 @@ def test_baseline_config_bf16_fwd_bwd(name, device):
     names = ("out", "dq", "dk", "dv")
     say(name, "ref max |x|", {n: round(r.abs().max().item(), 3) for n, r in zip(names, ref)})
     for n, a, r in zip(names, got, ref):
-        check_bf16(f"{name} {n}", a, r)
+        check_bf16(f"{name} {n}", a, r, summary=True)
 
 
 def test_bf16_against_reference_cast_points(device):
@@ -702,3 +702,56 @@ def test_phase_entry_points_match_the_fused_backward(dtype, name, device):
             torch.testing.assert_close(a, r, rtol=1e-5, atol=1e-5)
         else:
             check_bf16("phase entry points vs fused", a, r)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("hq, hkv", [(4, 2), (8, 1)])
+def test_stage_aligned_segments_packed_equal_alone_bitwise(mode, hq, hkv, device):
+    """A bf16 segment that starts on a 64-token stage boundary of a packed row gives, in
+    the forward and the backward, the bits it gives alone in a row of its own length
+    (the reference's packed-equals-separate property, tests/models/lfm2_5/test_encoder.py
+    :65-103, held exactly): each query (key) visits the segment's keys (queries) in the
+    same stages at the same positions, the other segments' pairs contribute exact zeros,
+    and the shift decisions of the forward are per query.  Segments that start off a
+    stage boundary sum in another order and meet the bf16 bar instead."""
+    rng = np.random.default_rng(40 + mode)
+    lengths = [100, 64, 1, 37, 200, 130, 65]
+    starts, pos = [], 0
+    for n in lengths:
+        starts.append(pos)
+        pos = -(-(pos + n) // 64) * 64 + 64 * int(rng.integers(0, 2))  # gaps of padding
+    t = pos + 23
+    seg = np.zeros((1, t), np.int32)
+    for i, (s0, n) in enumerate(zip(starts, lengths)):
+        seg[0, s0:s0 + n] = i + 1
+    say("stage-aligned segments", mode, (hq, hkv), t)
+    q, k, v, do = operands(rng, 1, t, hq, hkv, 64, torch.bfloat16, 0.5)
+    scale = 0.125
+
+    def run(qq, kk, vv, dd, ids):
+        ids = torch.tensor(ids, device=device)
+        plan = ops.block_map(ids, (ids != 0).to(torch.int32), mode, ids.shape[1], ids.shape[1])
+        out, lse = ops.attn_fwd(qq, kk, vv, plan, mode, scale)
+        return (out, lse, *ops.attn_bwd(qq, kk, vv, out, dd, lse, plan, mode, scale))
+
+    packed = run(q, k, v, do, seg)
+    for s0, n in zip(starts, lengths):
+        sl = slice(s0, s0 + n)
+        alone = run(*(x[:, sl].contiguous() for x in (q, k, v, do)), np.ones((1, n), np.int32))
+        got = (packed[0][:, sl], packed[1][:, :, sl], packed[2][:, sl], packed[3][:, sl],
+               packed[4][:, sl])
+        for name, a, r in zip(("out", "lse", "dq", "dk", "dv"), got, alone):
+            assert torch.equal(a, r), (n, s0, name, max_abs(a, r))
+    # the same segments shifted off the stage grid: equal to the bar, not bit for bit
+    shifted = np.zeros_like(seg)
+    shifted[0, 19:] = seg[0, :-19]
+    moved = run(*(torch.roll(x, 19, dims=1).contiguous() for x in (q, k, v, do)), shifted)
+    same = 0
+    for s0, n in zip(starts, lengths):
+        sl, sh = slice(s0, s0 + n), slice(s0 + 19, s0 + 19 + n)
+        got = (moved[0][:, sh], moved[2][:, sh], moved[3][:, sh], moved[4][:, sh])
+        ref = (packed[0][:, sl], packed[2][:, sl], packed[3][:, sl], packed[4][:, sl])
+        for name, a, r in zip(("out", "dq", "dk", "dv"), got, ref):
+            same += int(torch.equal(a, r))
+            check_bf16(f"shifted segment of {n} {name}", a, r.float())
+    say(f"segments 19 tokens off the stage grid: {same} of {4 * len(lengths)} tensors bit-identical")

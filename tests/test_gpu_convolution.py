@@ -95,11 +95,14 @@ def test_reference_gradient_fixtures_on_the_device(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("k", [1, 2, 3, 4, 7])
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("mode", ["centered", "causal"])
 def test_backward_matches_the_fp64_vjp(dtype, k, mode, device):
     """mf_segmented_conv_bwd through autograd against the analytic FP64 VJP (pinned by
-    the reference's gradient fixtures and central differences)."""
+    the reference's gradient fixtures and central differences).  Every width runs, so
+    each channels-per-thread form of the kernel does: 8 channels for K <= 4 and for bf16
+    K = 5 centered, 4 channels for the other wide filters (up to the 15-slot ring of
+    causal K = 8)."""
     rng = np.random.default_rng(40 + k)
     b, t, c = 3, 77, 24
     say("conv backward", mode, k, dtype)

@@ -82,7 +82,7 @@ def test_c4_full_shape(device):
         qq = q[row, 0].float()[:, None, :].contiguous()
         p = torch.softmax(torch.matmul(qq, kk.transpose(1, 2).contiguous()) * 0.125, dim=-1)
         ref[row, 0] = torch.matmul(p, vv)[:, 0]
-    check_bf16("C4", out, ref)
+    check_bf16("C4 out", out, ref, summary=True)
     del rng
 
 

@@ -109,3 +109,76 @@ def test_two_streams_at_once_equal_serial_calls(device):
         for rep in results[i]:
             for name, a, r in zip(("out", "lse", "dq", "dk", "dv"), rep, serial[i]):
                 assert torch.equal(a, r), (i, name)
+
+
+def _layout(rng, b, t):
+    seg = np.zeros((b, t), np.int32)
+    for row in range(b):
+        pos, sid = int(rng.integers(0, 40)), 1
+        while pos < t:
+            n = int(rng.integers(16, 500))
+            seg[row, pos:pos + n] = sid
+            pos, sid = pos + n, sid + 1
+    return seg
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_default_plan_cache_under_capture(mode, device):
+    """``packed_attention`` with ``plan=None`` (the default plan cache) captured into a
+    graph: each replay runs with the segment ids and mask then in the static buffers
+    (new layouts copied in between replays), so the captured step records its own
+    block map instead of reusing the warm-up's plan; eager calls after the capture on
+    the same tensors, and on a second stream, equal calls with a fresh plan."""
+    rng = np.random.default_rng(31 + mode)
+    b, t, hq, hkv, d = 2, 900, 4, 2, 64
+    scale = d ** -0.5
+    say("plan cache under capture", mode)
+    seg = torch.tensor(_layout(rng, b, t), device=device)
+    mask = (seg != 0).to(torch.int32)
+    g = torch.Generator(device=device).manual_seed(5)
+    mk = lambda h: torch.randn(b, t, h, d, generator=g, device=device).to(torch.bfloat16)  # noqa: E731
+    q, k, v, do = mk(hq), mk(hkv), mk(hkv), mk(hq)
+    for x in (q, k, v):
+        x.requires_grad_(True)
+
+    def step():
+        out = ops.packed_attention(q, k, v, mask, seg, mode, scale)
+        return (out, *torch.autograd.grad(out, (q, k, v), do))
+
+    def fresh():
+        with torch.no_grad():
+            plan = ops.block_map(seg, mask, mode, t, t)
+            out, lse = ops.attn_fwd(q.detach(), k.detach(), v.detach(), plan, mode, scale)
+            return (out, *ops.attn_bwd(q.detach(), k.detach(), v.detach(), out, do, lse, plan,
+                                       mode, scale))
+
+    ops.PLANS.clear()
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        step()  # warm-up: caches an eager plan of the first layout
+    torch.cuda.current_stream(device).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = step()
+    for trial in range(3):
+        new = torch.tensor(_layout(rng, b, t), device=device)
+        with torch.no_grad():
+            seg.copy_(new)
+            mask.copy_((new != 0).to(torch.int32))
+        graph.replay()
+        torch.cuda.synchronize(device)
+        want = fresh()
+        eager = step()
+        torch.cuda.synchronize(device)
+        for name, a, e, r in zip(("out", "dq", "dk", "dv"), captured, eager, want):
+            assert torch.equal(a, r), (trial, "replay", name)
+            assert torch.equal(e, r), (trial, "eager after capture", name)
+    other = torch.cuda.Stream(device)
+    other.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(other):
+        again = step()
+    torch.cuda.current_stream(device).wait_stream(other)
+    torch.cuda.synchronize(device)
+    for name, a, r in zip(("out", "dq", "dk", "dv"), again, fresh()):
+        assert torch.equal(a, r), ("second stream", name)

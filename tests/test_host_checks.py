@@ -97,3 +97,38 @@ def test_a_plan_for_another_call_is_rejected():
     plan = ops.Plan(torch.zeros(1, dtype=torch.uint8), 2, 8, 8, 0)
     with pytest.raises(ValueError, match="mask mode 0"):
         ops.attn_fwd(q, k, v, plan, 1, 0.125)
+
+
+def test_strided_views_are_refused_before_any_launch():
+    """The kernels read operands as dense arrays from their data pointers: a slice or a
+    transposed view is refused by every op that takes raw tensors (the drop-in functions
+    pass contiguous copies)."""
+    q, k, v = _qkv(t=16)
+    plan = ops.Plan(torch.zeros(1, dtype=torch.uint8), 2, 16, 16, 1)
+    strided_q = torch.zeros(2, 16, 8, 64, dtype=q.dtype)[:, :, ::2]
+    transposed_k = torch.zeros(2, 2, 16, 64, dtype=k.dtype).transpose(1, 2)
+    assert not strided_q.is_contiguous() and not transposed_k.is_contiguous()
+    with pytest.raises(ValueError, match="must be contiguous"):
+        ops.attn_fwd(strided_q, k, v, plan, 1, 0.125)
+    with pytest.raises(ValueError, match="must be contiguous"):
+        ops.attn_fwd(q, transposed_k, v, plan, 1, 0.125)
+    lse = torch.zeros(2, 4, 16)
+    out = torch.zeros_like(q)
+    dout_view = torch.zeros(2, 16, 8, 64, dtype=q.dtype)[:, :, 4:]
+    with pytest.raises(ValueError, match="must be contiguous"):
+        ops.attn_bwd(q, k, v, out, dout_view, lse, plan, 1, 0.125)
+    with pytest.raises(ValueError, match="must be contiguous"):
+        ops.attn_bwd(q, k, v, out, torch.zeros_like(q), lse.transpose(1, 2).contiguous()
+                     .transpose(1, 2), plan, 1, 0.125)
+    ws = ops.bwd_workspace(q)
+    with pytest.raises(ValueError, match="must be contiguous"):
+        ops.attn_bwd_dq(q, k, v, torch.zeros_like(q), lse, plan, 1, 0.125, ws,
+                        torch.zeros(2, 16, 8, 64, dtype=q.dtype)[:, :, ::2])
+    with pytest.raises(ValueError, match="must be contiguous"):
+        ops.attn_bwd_dkdv(q, k, v, torch.zeros_like(q), lse, plan, 1, 0.125, ws, transposed_k,
+                          torch.zeros_like(v))
+    with pytest.raises(ValueError, match="at least"):
+        ops.attn_bwd_dkdv(q, k, v, torch.zeros_like(q), lse, plan, 1, 0.125, ws[:8],
+                          torch.zeros_like(k), torch.zeros_like(v))
+    with pytest.raises(ValueError, match="lse must be"):
+        ops.attn_bwd_delta(out, torch.zeros_like(q), torch.zeros(2, 4, 15), ws)
