@@ -50,6 +50,7 @@ struct BwdArgs {
   int causal;
   int fuse_delta;  // bf16 dq computes D = rowsum(dO * O) itself and writes -D and lse2
   float scale, scale_log2;
+  FastDiv div_nh, div_hchunks, div_nq, div_hkv, div_nk;  // Hkv * hchunks, hchunks, nq, Hkv, nk
 };
 
 constexpr int kStep = 64;
@@ -146,12 +147,13 @@ __global__ __launch_bounds__(256) void bwd_dq_f32_kernel(BwdArgs a) {
   const int half = lane >> 5;
   // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
   const int nh = a.Hkv * a.hchunks;
-  const int hr = uniform(blockIdx.x % nh);
-  const int kvh = uniform(hr / a.hchunks);
-  const int hc = uniform(hr % a.hchunks);
-  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
-  const int b = uniform(item / a.nq);
-  const int qt = uniform(item % a.nq);
+  const int slot = uniform(fast_div(blockIdx.x, a.div_nh));
+  const int hr = uniform(blockIdx.x - slot * nh);
+  const int kvh = uniform(fast_div(hr, a.div_hchunks));
+  const int hc = uniform(hr - kvh * a.hchunks);
+  const int item = ld_const(a.qorder, slot);  // (row, query tile), longest first
+  const int b = uniform(fast_div(item, a.div_nq));
+  const int qt = uniform(item - b * a.nq);
   const int qpos = qt * kTile + wave * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
   const bool qvalid = qpos < a.T;
@@ -355,10 +357,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(BwdArgs a) {
   const int wave = threadIdx.x >> 6;
   const int half = lane >> 5;
   // 1-D grid: (key-tile item in launch order, kvh), heads fastest
-  const int kvh = uniform(blockIdx.x % a.Hkv);
-  const int item = ld_const(a.korder, blockIdx.x / a.Hkv);  // (row, key tile), longest first
-  const int b = uniform(item / a.nk);
-  const int kt = uniform(item % a.nk);
+  const int slot = uniform(fast_div(blockIdx.x, a.div_hkv));
+  const int kvh = uniform(blockIdx.x - slot * a.Hkv);
+  const int item = ld_const(a.korder, slot);  // (row, key tile), longest first
+  const int b = uniform(fast_div(item, a.div_nk));
+  const int kt = uniform(item - b * a.nk);
   const int kpos = kt * kTile + wave * 32 + (lane & 31);
   const int mykid = a.kid[(size_t)b * a.tk_pad + kpos];
   const bool kvalid = kpos < a.S;
@@ -487,12 +490,13 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   const int half = lane >> 5;
   // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
   const int nh = a.Hkv * a.hchunks;
-  const int hr = uniform(blockIdx.x % nh);
-  const int kvh = uniform(hr / a.hchunks);
-  const int hc = uniform(hr % a.hchunks);
-  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
-  const int b = uniform(item / a.nq);
-  const int qt = uniform(item % a.nq);
+  const int slot = uniform(fast_div(blockIdx.x, a.div_nh));
+  const int hr = uniform(blockIdx.x - slot * nh);
+  const int kvh = uniform(fast_div(hr, a.div_hchunks));
+  const int hc = uniform(hr - kvh * a.hchunks);
+  const int item = ld_const(a.qorder, slot);  // (row, query tile), longest first
+  const int b = uniform(fast_div(item, a.div_nq));
+  const int qt = uniform(item - b * a.nq);
   const int head = kvh * a.G + hc * HPW + (wave >> 2);
   const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
@@ -515,6 +519,8 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   const char* kg = reinterpret_cast<const char*>(a.k) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
   const char* vg = reinterpret_cast<const char*>(a.v) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
 
+  // (the precomputed-offset form of kv_dma measured 2-5% slower here: its
+  // offsets cost dq registers that it then spills)
   auto issue = [&](int s, char* stage) {
     kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage);
   };
@@ -707,10 +713,11 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   const int wave = uniform(tid >> 6);
   const int half = lane >> 5;
   // 1-D grid: (key-tile item in launch order, kvh), heads fastest
-  const int kvh = uniform(blockIdx.x % a.Hkv);
-  const int item = ld_const(a.korder, blockIdx.x / a.Hkv);  // (row, key tile), longest first
-  const int b = uniform(item / a.nk);
-  const int kt = uniform(item % a.nk);
+  const int slot = uniform(fast_div(blockIdx.x, a.div_hkv));
+  const int kvh = uniform(blockIdx.x - slot * a.Hkv);
+  const int item = ld_const(a.korder, slot);  // (row, key tile), longest first
+  const int b = uniform(fast_div(item, a.div_nk));
+  const int kt = uniform(item - b * a.nk);
   const int kpos = kt * kTile + (wave & 3) * 32 + (lane & 31);
   const int mykid = a.kid[(size_t)b * a.tk_pad + kpos];
   const bool kvalid = kpos < a.S;
@@ -978,6 +985,11 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   a.causal = mode == 0;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
+  a.div_nh = make_fastdiv(a.Hkv * a.hchunks);
+  a.div_hchunks = make_fastdiv(a.hchunks);
+  a.div_nq = make_fastdiv(a.nq);
+  a.div_hkv = make_fastdiv(a.Hkv);
+  a.div_nk = make_fastdiv(a.nk);
   const size_t rows = (size_t)batch * T * Hq;
   const unsigned dgrid = (unsigned)((rows + 255) / 256);
   // bf16 with both the delta and the dq phase: the dq kernel, which holds

@@ -34,6 +34,7 @@ struct FwdArgs {
   int nq, nk, tq_pad, tk_pad;
   int causal;
   float scale, scale_log2;
+  FastDiv div_nh, div_hchunks, div_nq;  // Hkv * hchunks, hchunks, nq
   // query prologue fused into the bf16 kernel's query loads (ROPE instances)
   const void* q_gain;           // [64], tensor dtype
   const int32_t* positions;     // [B, T] or null (0 .. T-1 on every row)
@@ -95,12 +96,13 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_kernel(FwdArgs a) {
   const int half = lane >> 5;
   // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
   const int nh = a.Hkv * a.hchunks;
-  const int hr = uniform(blockIdx.x % nh);
-  const int kvh = uniform(hr / a.hchunks);
-  const int hc = uniform(hr % a.hchunks);
-  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
-  const int b = uniform(item / a.nq);
-  const int qt = uniform(item % a.nq);
+  const int slot = uniform(fast_div(blockIdx.x, a.div_nh));
+  const int hr = uniform(blockIdx.x - slot * nh);
+  const int kvh = uniform(fast_div(hr, a.div_hchunks));
+  const int hc = uniform(hr - kvh * a.hchunks);
+  const int item = ld_const(a.qorder, slot);  // (row, query tile), longest first
+  const int b = uniform(fast_div(item, a.div_nq));
+  const int qt = uniform(item - b * a.nq);
   const int qpos = qt * kTile + wave * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
   const bool qvalid = qpos < a.T;
@@ -366,12 +368,13 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   const int half = lane >> 5;
   // 1-D grid: (query-tile item in launch order, kvh, head chunk), heads fastest
   const int nh = a.Hkv * a.hchunks;
-  const int hr = uniform(blockIdx.x % nh);
-  const int kvh = uniform(hr / a.hchunks);
-  const int hc = uniform(hr % a.hchunks);
-  const int item = ld_const(a.qorder, blockIdx.x / nh);  // (row, query tile), longest first
-  const int b = uniform(item / a.nq);
-  const int qt = uniform(item % a.nq);
+  const int slot = uniform(fast_div(blockIdx.x, a.div_nh));
+  const int hr = uniform(blockIdx.x - slot * nh);
+  const int kvh = uniform(fast_div(hr, a.div_hchunks));
+  const int hc = uniform(hr - kvh * a.hchunks);
+  const int item = ld_const(a.qorder, slot);  // (row, query tile), longest first
+  const int b = uniform(fast_div(item, a.div_nq));
+  const int qt = uniform(item - b * a.nq);
   const int head = kvh * a.G + hc * HPW + (wave >> 2);
   const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
@@ -406,8 +409,9 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   const char* kg = reinterpret_cast<const char*>(a.k) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
   const char* vg = reinterpret_cast<const char*>(a.v) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
 
+  const KvLanes<W> kv_lane = kv_lanes<W>(row_stride, wave);
   auto issue = [&](int s, char* stage) {
-    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage);
+    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage, kv_lane);
   };
 
   // Sub-block classification inside PARTIAL tiles.  A wave's 32 queries
@@ -427,8 +431,8 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     return s;
   };
 
-  // masks and shifted scores of one block; returns its row max (both halves)
-  auto prep_block = [&](f32x16& s, const int* kids_lds, int kb, int kb2, bool mask_ids, bool diag) {
+  // masks of one block; returns the row max of its raw scores (both halves)
+  auto mask_block = [&](f32x16& s, const int* kids_lds, int kb, int kb2, bool mask_ids, bool diag) {
     if (mask_ids) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
@@ -444,19 +448,15 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
       for (int r = 0; r < 16; ++r)
         s[r] = kb + kb2 * 32 + acc_row(r, lane) <= qpos ? s[r] : kNegInf;
     }
-    // shift first: FMA results are canonical, so the max needs no NaN
-    // quieting and folds into v_max3
-#pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = fmaf(s[r], c, -shift);
     float mx = fmaxf(s[0], s[1]);
 #pragma unroll
     for (int r = 2; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[r]), s[r + 1]);
     return mx;
   };
-  // exponentials, row sums and O += P V of one block
+  // probabilities 2^(s c - shift), row sums and O += P V of one block
   auto finish_pv = [&](f32x16& s, const char* vt, int kb2) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(s[r]);
+    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], c, -shift));
     const bf16x8 p0 = pack8(s, 0), p1 = pack8(s, 8);
     // row sum of the bf16 probabilities that P V uses: one v_dot2 with
     // (1, 1) per pair (copied through scalars: __builtin_bit_cast of a
@@ -511,33 +511,32 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     f32x16 s0, s1;
     if (run[0]) s0 = scores(kt, 0);
     if (run[1]) s1 = scores(kt, 1);
-    // One shift decision for the step's two blocks, taken before either
-    // block's probabilities exist.  A growing lane moves its shift to the new
-    // max: d > 0 and finite, so alpha = 2^-d is finite (a lane with no valid
-    // key yet has l = 0, O = 0).
+    // One shift decision for the step's two blocks, taken on the raw scores
+    // before either block's probabilities exist: c > 0 and the rounding of
+    // an FMA is monotone, so fma(max s, c, -shift) is exactly the max of the
+    // shifted scores.  A growing lane moves its shift to the new max: d > 0
+    // and finite, so alpha = 2^-d is finite (a lane with no valid key yet has
+    // l = 0, O = 0).  At a tile's first step every lane has l = 0 and O = 0,
+    // so the rescale is skipped there.
     float mx = kNegInf;
-    if (run[0]) mx = prep_block(s0, kids_lds, kb, 0, mask_ids[0], diag[0]);
-    if (run[1]) mx = fmaxf(mx, prep_block(s1, kids_lds, kb, 1, mask_ids[1], diag[1]));
-    mx = halves_max(mx);
+    if (run[0]) mx = mask_block(s0, kids_lds, kb, 0, mask_ids[0], diag[0]);
+    if (run[1]) mx = fmaxf(mx, mask_block(s1, kids_lds, kb, 1, mask_ids[1], diag[1]));
+    mx = fmaf(halves_max(mx), c, -shift);
     const bool grow = mx > lag;
     if (__any(grow)) {
       const float d = grow ? mx : 0.f;
-      const float alpha = fast_exp2(-d);
       shift += d;
       lag = grow ? 8.f : lag;
-      l0 *= alpha;
-      l1 *= alpha;
+      if (step > 0) {
+        const float alpha = fast_exp2(-d);
+        l0 *= alpha;
+        l1 *= alpha;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        oacc[0][r] *= alpha;
-        oacc[1][r] *= alpha;
+        for (int r = 0; r < 16; ++r) {
+          oacc[0][r] *= alpha;
+          oacc[1][r] *= alpha;
+        }
       }
-      if (run[0])
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s0[r] -= d;
-      if (run[1])
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s1[r] -= d;
     }
     if (run[0]) finish_pv(s0, vt, 0);
     if (run[1]) finish_pv(s1, vt, 1);
@@ -624,6 +623,9 @@ static FwdArgs fwd_args(const void* q, const void* k, const void* v, int batch, 
   a.causal = mode == 0;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
+  a.div_nh = make_fastdiv(a.Hkv * a.hchunks);
+  a.div_hchunks = make_fastdiv(a.hchunks);
+  a.div_nq = make_fastdiv(a.nq);
   return a;
 }
 

@@ -129,6 +129,32 @@ __device__ __forceinline__ void st_u32x4(void* p, const u32x4& v) {
 // dependent loads become vector loads and the work loops become divergent.
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// Division of integers in [0, 2^31) by a divisor d >= 1 fixed at launch, by
+// the round-up method of Granlund and Montgomery ("Division by invariant
+// integers using multiplication", 1994): with shr = ceil(log2 d) and
+// m = 2^32 + mul = floor(2^(32 + shr) / d) + 1, x / d = floor(x m / 2^(32 + shr)).
+// m d exceeds 2^(32 + shr) by e in (0, d], so x m / 2^(32 + shr) exceeds x / d
+// by x e / (d 2^(32 + shr)) < 1 / d for x < 2^32, which never carries the
+// quotient past the next integer.  umulhi(x, mul) < x keeps the 32-bit sum
+// below 2^32 for x < 2^31.  The grid-index decompositions use it in place of
+// the compiler's generic division (about 30 dependent scalar instructions).
+struct FastDiv {
+  uint32_t d, mul, shr;
+};
+
+inline FastDiv make_fastdiv(int d) {
+  FastDiv f;
+  f.d = (uint32_t)d;
+  f.shr = 0;
+  while ((1ull << f.shr) < f.d) ++f.shr;
+  f.mul = (uint32_t)(((1ull << 32) * ((1ull << f.shr) - f.d)) / f.d + 1);
+  return f;
+}
+
+__device__ __forceinline__ int fast_div(int x, const FastDiv& f) {
+  return (int)((__umulhi((uint32_t)x, f.mul) + (uint32_t)x) >> f.shr);
+}
+
 // Read of a wave-uniform index from memory that is immutable for the whole
 // kernel (the plan's work lists): the constant address space lets the
 // compiler use a scalar load, which does not queue behind the vector loads

@@ -127,6 +127,28 @@ struct KvDma {
   static constexpr int kGroups = 8 / W;            // 8-row groups per tile per wave
 };
 
+// Per-lane source offsets of a wave's kv_dma rows, relative to the stage's
+// first key row: group j covers tile rows r0 = 8 (wave + W j) .. r0 + 7, and
+// the lane fetches chunk (lane & 7) ^ swz(r) of row r = r0 + lane / 8.
+// Computed once per kernel; the stages that lie inside the tensor then issue
+// their DMAs with scalar address arithmetic only.
+template <int W>
+struct KvLanes {
+  uint32_t off[KvDma<W>::kGroups];
+};
+
+template <int W>
+__device__ __forceinline__ KvLanes<W> kv_lanes(uint32_t row_stride, int wave) {
+  KvLanes<W> l;
+  const int lane = __lane_id();
+#pragma unroll
+  for (int j = 0; j < KvDma<W>::kGroups; ++j) {
+    const int r = 8 * (wave + W * j) + (lane >> 3);
+    l.off[j] = (uint32_t)r * row_stride + (uint32_t)(((lane & 7) ^ swz(r)) * 16);
+  }
+  return l;
+}
+
 // DMA of keys kb .. kb+63 (K rows, V rows, canonical ids) into one stage.
 // kid_row must hold at least kb + 64 entries (the plan pads ids to whole tiles).
 template <int W>
@@ -138,6 +160,31 @@ __device__ __forceinline__ void kv_dma(const char* kg, const char* vg, uint32_t 
     const int r0 = 8 * (wave + W * j);
     dma_rows8(kg, row_stride, kb, r0, S - 1, stage);
     dma_rows8(vg, row_stride, kb, r0, S - 1, stage + kTileBytes);
+  }
+}
+
+// The same DMA with the lanes' source offsets precomputed (kv_lanes).
+// A stage that reaches past key S - 1 re-reads row S - 1 for those rows.
+template <int W>
+__device__ __forceinline__ void kv_dma(const char* kg, const char* vg, uint32_t row_stride, int S,
+                                       const int* kid_row, int kb, int wave, char* stage,
+                                       const KvLanes<W>& lanes) {
+  if (wave == 0) dma_word64(kid_row + kb, 4u * __lane_id(), stage + 2 * kTileBytes);
+  if (kb + kKvStep <= S) {
+    const uint32_t first = (uint32_t)kb * row_stride;
+#pragma unroll
+    for (int j = 0; j < KvDma<W>::kGroups; ++j) {
+      const uint32_t dst = uniform((int)lds_offset(stage + 8 * (wave + W * j) * kRowBytes));
+      dma16(kg + first, lanes.off[j], dst);
+      dma16(vg + first, lanes.off[j], dst + kTileBytes);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KvDma<W>::kGroups; ++j) {
+      const int r0 = 8 * (wave + W * j);
+      dma_rows8(kg, row_stride, kb, r0, S - 1, stage);
+      dma_rows8(vg, row_stride, kb, r0, S - 1, stage + kTileBytes);
+    }
   }
 }
 
