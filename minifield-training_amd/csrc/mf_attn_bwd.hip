@@ -50,7 +50,7 @@ struct BwdArgs {
   int causal;
   int fuse_delta;  // bf16 dq computes D = rowsum(dO * O) itself and writes -D and lse2
   float scale, scale_log2;
-  FastDiv div_nh, div_hchunks, div_nq, div_hkv, div_nk;  // Hkv * hchunks, hchunks, nq, Hkv, nk
+  FastDiv div_nh, div_hchunks, div_nq, div_hkv, div_nk, div_g;  // Hkv * hchunks, hchunks, nq, Hkv, nk, G
 };
 
 constexpr int kStep = 64;
@@ -511,7 +511,6 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   const int count = ld_const(a.qcnt, b * a.nq + qt);
   const int* list = a.qlist + ((size_t)b * a.nq + qt) * 2 * a.nk;
   const int nsteps = count;  // one 64-key stage per list entry
-  auto step_kb = [&](int s) { return (ld_const(list, s) >> 2) * kKvStep; };
   const int tr_row = tr_row_of(lane);
   const int tr_col = tr_col_of(lane);
   const int* kid_row = a.kid + (size_t)b * a.tk_pad;
@@ -521,8 +520,8 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
 
   // (the precomputed-offset form of kv_dma measured 2-5% slower here: its
   // offsets cost dq registers that it then spills)
-  auto issue = [&](int s, char* stage) {
-    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage);
+  auto issue = [&](int entry, char* stage) {
+    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, (entry >> 2) * kKvStep, wave, stage);
   };
 
   // Sub-block classification inside PARTIAL tiles, as in the forward: a
@@ -567,8 +566,7 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     }
   };
 
-  auto compute = [&](int step, const char* stage) {
-    const int entry = ld_const(list, step);
+  auto compute = [&](int entry, const char* stage) {
     const int kb = (entry >> 2) * kKvStep;
     const bool partial = (entry & 3) == 1;
     const char* kt = stage;
@@ -597,16 +595,23 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   // Ring of two 128-key slots (as in the forward): slot i+1's DMAs are issued
   // right after the barrier that opens slot i; whole pairs of slots, with the
   // computes past the end skipped.
-  auto issue_slot = [&](int i, char* slot) {
-    if (2 * i < nsteps) issue(2 * i, slot);
-    if (2 * i + 1 < nsteps) issue(2 * i + 1, slot + kStageBytes);
+  auto issue_slot = [&](int i, int e0, int e1, char* slot) {
+    if (2 * i < nsteps) issue(e0, slot);
+    if (2 * i + 1 < nsteps) issue(e1, slot + kStageBytes);
   };
   const int nslots = (nsteps + 1) >> 1;
   // Both slots and the query-side rows (q, dO, lse, O for D) are in flight
   // together before the first wait; after that slot i+1's DMAs are issued
-  // when slot i opens.
-  issue_slot(0, slotA);
-  issue_slot(1, slotB);
+  // when slot i opens.  The list entries a pair of slots needs (steps
+  // 2i .. 2i+5) arrive in one scalar load of eight; the read may run up to 7
+  // entries past the list's end, into the plan's next section (query lists
+  // are followed by the key-tile counts), and entries at or past nsteps are
+  // never used.
+  {
+    const i32x8u e = ld_const8(list, 0);
+    issue_slot(0, e[0], e[1], slotA);
+    issue_slot(1, e[2], e[3], slotB);
+  }
   {
     const size_t row = (((size_t)b * a.T + min(qpos, a.T - 1)) * a.Hq + head) * kD + 8 * half;
     const bf16* qs = reinterpret_cast<const bf16*>(a.q) + row;
@@ -650,16 +655,17 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   lse2 = qactive ? lse_raw * kLog2e : kPosInf;
   dlt = qactive ? dlt_raw : 0.f;
   for (int i = 0; i < nslots; i += 2) {
+    const i32x8u e = ld_const8(list, 2 * i);
     wait_vmcnt<0>();
     barrier();
-    if (i > 0) issue_slot(i + 1, slotB);
-    compute(2 * i, slotA);
-    if (2 * i + 1 < nsteps) compute(2 * i + 1, slotA + kStageBytes);
+    if (i > 0) issue_slot(i + 1, e[2], e[3], slotB);
+    compute(e[0], slotA);
+    if (2 * i + 1 < nsteps) compute(e[1], slotA + kStageBytes);
     wait_vmcnt<0>();
     barrier();
-    issue_slot(i + 2, slotA);
-    if (2 * i + 2 < nsteps) compute(2 * i + 2, slotB);
-    if (2 * i + 3 < nsteps) compute(2 * i + 3, slotB + kStageBytes);
+    issue_slot(i + 2, e[4], e[5], slotA);
+    if (2 * i + 2 < nsteps) compute(e[2], slotB);
+    if (2 * i + 3 < nsteps) compute(e[3], slotB + kStageBytes);
   }
   wait_vmcnt<0>();
 
@@ -748,8 +754,9 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   // DMA of iteration `it` (query rows qb .. qb+63 of one head) into a stage.
   auto issue = [&](int it, char* stage) {
     it = min(it, niters - 1);
-    const int entry = ld_const(list, it / hps);
-    const int hj = it % hps;
+    const int si = fast_div(it, a.div_g);  // hps == G
+    const int entry = ld_const(list, si);
+    const int hj = it - si * hps;
     const int qb = (entry >> 2) * kKvStep;
     // the word arrays first, so the short step wait covers them
     if (wave < Q::kWordArrays) {
@@ -860,7 +867,7 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   };
 
   auto compute = [&](int it, const char* stage) {
-    const int entry = ld_const(list, it / hps);
+    const int entry = ld_const(list, fast_div(it, a.div_g));
     const int qb = (entry >> 2) * kKvStep;
     const bool partial = (entry & 3) == 1;
     const char* qt = stage;
@@ -990,6 +997,7 @@ hipError_t launch_attn_bwd(const void* q, const void* k, const void* v, const vo
   a.div_nq = make_fastdiv(a.nq);
   a.div_hkv = make_fastdiv(a.Hkv);
   a.div_nk = make_fastdiv(a.nk);
+  a.div_g = make_fastdiv(a.G);
   const size_t rows = (size_t)batch * T * Hq;
   const unsigned dgrid = (unsigned)((rows + 255) / 256);
   // bf16 with both the delta and the dq phase: the dq kernel, which holds

@@ -401,7 +401,6 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   const int count = ld_const(a.qcnt, b * a.nq + qt);
   const int* list = a.qlist + ((size_t)b * a.nq + qt) * 2 * a.nk;
   const int nsteps = count;  // one 64-key stage per list entry
-  auto step_kb = [&](int s) { return (ld_const(list, s) >> 2) * kStepK; };
   const int tr_row = tr_row_of(lane);
   const int tr_col = tr_col_of(lane);
   const int* kid_row = a.kid + (size_t)b * a.tk_pad;
@@ -410,8 +409,8 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   const char* vg = reinterpret_cast<const char*>(a.v) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
 
   const KvLanes<W> kv_lane = kv_lanes<W>(row_stride, wave);
-  auto issue = [&](int s, char* stage) {
-    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, step_kb(min(s, nsteps - 1)), wave, stage, kv_lane);
+  auto issue = [&](int entry, char* stage) {
+    kv_dma<W>(kg, vg, row_stride, a.S, kid_row, (entry >> 2) * kStepK, wave, stage, kv_lane);
   };
 
   // Sub-block classification inside PARTIAL tiles.  A wave's 32 queries
@@ -484,8 +483,7 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   // softmax work, so the second block's MFMAs run under the first block's
   // masks and max; both blocks share one shift decision; the first block's
   // P V then runs under the second block's exponentials.
-  auto compute = [&](int step, const char* stage) {
-    const int entry = ld_const(list, step);
+  auto compute = [&](int step, int entry, const char* stage) {
     const int kb = (entry >> 2) * kStepK;
     const bool partial = (entry & 3) == 1;
     const char* kt = stage;
@@ -545,26 +543,35 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   // Ring of two 128-key slots: the DMAs of slot i+1 are issued right after
   // the barrier that opens slot i, so they have the compute of slot i (four
   // 32-key blocks) to land, and one barrier serves 128 keys.
-  auto issue_slot = [&](int i, char* slot) {
-    if (2 * i < nsteps) issue(2 * i, slot);
-    if (2 * i + 1 < nsteps) issue(2 * i + 1, slot + kStageBytes);
+  auto issue_slot = [&](int i, int e0, int e1, char* slot) {
+    if (2 * i < nsteps) issue(e0, slot);
+    if (2 * i + 1 < nsteps) issue(e1, slot + kStageBytes);
   };
   const int nslots = (nsteps + 1) >> 1;
-  issue_slot(0, slotA);
+  // The list entries a pair of slots needs (steps 2i .. 2i+5) arrive in one
+  // scalar load of eight, issued before the pair's first wait.  The read may
+  // run up to 7 entries past the list's end, into the plan's next section
+  // (query lists are followed by the key-tile counts); entries at or past
+  // nsteps are never used.
+  {
+    const i32x8u e = ld_const8(list, 0);
+    issue_slot(0, e[0], e[1], slotA);
+  }
   // Whole pairs of slots; the computes past the end are skipped rather than
   // leaving the loop mid-pair (a mid-pair exit gives the accumulators two
   // exit paths, resolved with register copies).
   for (int i = 0; i < nslots; i += 2) {
+    const i32x8u e = ld_const8(list, 2 * i);
     wait_vmcnt<0>();
     barrier();
-    issue_slot(i + 1, slotB);
-    compute(2 * i, slotA);
-    if (2 * i + 1 < nsteps) compute(2 * i + 1, slotA + kStageBytes);
+    issue_slot(i + 1, e[2], e[3], slotB);
+    compute(2 * i, e[0], slotA);
+    if (2 * i + 1 < nsteps) compute(2 * i + 1, e[1], slotA + kStageBytes);
     wait_vmcnt<0>();
     barrier();
-    issue_slot(i + 2, slotA);
-    if (2 * i + 2 < nsteps) compute(2 * i + 2, slotB);
-    if (2 * i + 3 < nsteps) compute(2 * i + 3, slotB + kStageBytes);
+    issue_slot(i + 2, e[4], e[5], slotA);
+    if (2 * i + 2 < nsteps) compute(2 * i + 2, e[2], slotB);
+    if (2 * i + 3 < nsteps) compute(2 * i + 3, e[3], slotB + kStageBytes);
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 

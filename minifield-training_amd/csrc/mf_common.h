@@ -163,6 +163,14 @@ __device__ __forceinline__ int ld_const(const int* p, int i) {
   return ((const __attribute__((address_space(4))) int*)(p))[__builtin_amdgcn_readfirstlane(i)];
 }
 
+// Eight consecutive entries p[i .. i+7] of such an array in one scalar load
+// (i wave-uniform; only dword alignment is required of p + i).  The caller
+// guarantees that the 32 bytes lie inside the allocation.
+typedef int i32x8u __attribute__((ext_vector_type(8), aligned(4)));
+__device__ __forceinline__ i32x8u ld_const8(const int* p, int i) {
+  return *((const __attribute__((address_space(4))) i32x8u*)(p + __builtin_amdgcn_readfirstlane(i)));
+}
+
 // Wait for every outstanding memory operation.  Used once, after the
 // per-wave operands that stay in registers for the whole kernel are loaded:
 // the compiler's wait insertion cannot see across the work loop's back edge
