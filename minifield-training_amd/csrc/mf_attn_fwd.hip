@@ -378,7 +378,6 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   const int head = kvh * a.G + hc * HPW + (wave >> 2);
   const int qpos = qt * kTile + (wave & 3) * 32 + (lane & 31);
   const int myqid = a.qid[(size_t)b * a.tq_pad + qpos];
-  const bool qvalid = qpos < a.T;
 
   bf16x8 qf[4];
   {
@@ -575,24 +574,31 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 
-  const bool qactive = qvalid && myqid != 0;
+  // the lane's query position and half again from the lane id: recomputing
+  // them is cheaper than keeping them (the compiler would spill them) across
+  // the loop
+  const int elane = fresh_lane_id();
+  const int ehalf = elane >> 5;
+  const int eqpos = qt * kTile + (wave & 3) * 32 + (elane & 31);
+  const bool eqvalid = eqpos < a.T;
+  const bool qactive = eqvalid && myqid != 0;
   const float lt = halves_sum(l0 + l1);
   const bool has = qactive && lt > 0.f;
   const float inv = has ? 1.f / lt : 0.f;
-  if (qvalid) {
+  if (eqvalid) {
     // natural-log LSE: shift / log2(e) + ln(l)
-    if (half == 0)
-      a.lse[((size_t)b * a.Hq + head) * a.T + qpos] = has ? fmaf(shift, kLn2, __logf(lt)) : kPosInf;
+    if (ehalf == 0)
+      a.lse[((size_t)b * a.Hq + head) * a.T + eqpos] = has ? fmaf(shift, kLn2, __logf(lt)) : kPosInf;
 #pragma unroll
     for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        const int d0 = db * 32 + 8 * g4 + 4 * half;
+        const int d0 = db * 32 + 8 * g4 + 4 * ehalf;
         bf16x4 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (bf16)(has ? oacc[db][g4 * 4 + i] * inv : 0.f);
         *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.out) +
-                                   (((size_t)b * a.T + qpos) * a.Hq + head) * kD + d0) = o;
+                                   (((size_t)b * a.T + eqpos) * a.Hq + head) * kD + d0) = o;
       }
   }
 }

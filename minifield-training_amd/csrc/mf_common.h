@@ -124,6 +124,15 @@ __device__ __forceinline__ void st_u32x4(void* p, const u32x4& v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// The lane id, computed afresh by instructions the compiler cannot merge
+// with an earlier copy: code after a long loop uses it instead of keeping
+// lane-derived values alive (or spilled to scratch) across the loop.
+__device__ __forceinline__ int fresh_lane_id() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
 // A wave-uniform integer forced into a scalar register.  Index arithmetic
 // on blockIdx with runtime divisors is lowered through VALU; without this the
 // dependent loads become vector loads and the work loops become divergent.

@@ -79,22 +79,11 @@ def test_device_code_makes_no_calls(tmp_path):
     assert not [k for k in funcs if k.startswith("__o")], sorted(k for k in funcs if k.startswith("__o"))
 
 
-def test_scratch_is_one_spill_outside_the_key_loop(tmp_path):
-    """Register spills go to scratch memory in HBM.  The two-head forwards (with and without
-    the query's norm and RoPE fused in) keep at most two registers there across their key
-    loop: stored before the loop's first barrier, loaded after its last.  No other kernel
-    touches scratch."""
+def test_no_kernel_touches_scratch(tmp_path):
+    """Register spills go to scratch memory in HBM (a reload costs a memory round trip, and
+    4 bytes per lane of write traffic).  No kernel of the library spills: every value that
+    the work loops do not need is recomputed after them instead."""
     funcs = _disassembly(tmp_path)
     use = {k: [l for l in lines if "scratch_" in l] for k, lines in funcs.items()}
-    use = {k: v for k, v in use.items() if v}
-    fwd2 = [k for k in use if k.startswith("_ZN2mf20attn_fwd_bf16_kernelILi2E")]
-    assert set(use) <= set(fwd2), sorted(set(use) - set(fwd2))
-    for k in fwd2:
-        lines = funcs[k]
-        assert len(use[k]) <= 4, (k, use[k])
-        bars = [i for i, l in enumerate(lines) if "s_barrier" in l]
-        for i, l in enumerate(lines):
-            if "scratch_store" in l:
-                assert i < bars[0], (k, l)
-            elif "scratch_load" in l:
-                assert i > bars[-1], (k, l)
+    use = {k: v[:2] for k, v in use.items() if v}
+    assert not use, use
