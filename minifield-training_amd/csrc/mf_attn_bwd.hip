@@ -644,10 +644,6 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
       }
     }
     dlt_raw = halves_sum(part);
-    if (qvalid && half == 0) {
-      a.ndelta[li] = -dlt_raw;
-      a.lse2[li] = lse_raw * kLog2e;
-    }
   } else {
     dlt_raw = -a.ndelta[li];
   }
@@ -669,17 +665,31 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   }
   wait_vmcnt<0>();
 
-  if (!qvalid) return;
+  // the lane's query position and half again from a fresh lane id
+  // (cheaper than keeping them across the loop)
+  const int elane = fresh_lane_id();
+  const int ehalf = elane >> 5;
+  const int eqpos = qt * kTile + (wave & 3) * 32 + (elane & 31);
+  if (eqpos >= a.T) return;
+  // -D and lse * log2(e) for the dk/dv kernel, stored after the loop rather
+  // than before it (a store in flight would hold up the first stage's wait).
+  // The values the loop used: an inactive row's are 0 and +inf, which dk/dv
+  // never combines with a non-zero probability.
+  if (a.fuse_delta && ehalf == 0) {
+    const size_t lj = ((size_t)b * a.Hq + head) * a.T + eqpos;
+    a.ndelta[lj] = -dlt;
+    a.lse2[lj] = lse2;
+  }
 #pragma unroll
   for (int db = 0; db < 2; ++db)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const int d0 = db * 32 + 8 * g4 + 4 * half;
+      const int d0 = db * 32 + 8 * g4 + 4 * ehalf;
       bf16x4 o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = (bf16)(qactive ? dqacc[db][g4 * 4 + i] * a.scale : 0.f);
       *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dq) +
-                                 (((size_t)b * a.T + qpos) * a.Hq + head) * kD + d0) = o;
+                                 (((size_t)b * a.T + eqpos) * a.Hq + head) * kD + d0) = o;
     }
 }
 
