@@ -600,8 +600,13 @@ def main() -> int:
     decode = decode_leg(args.steps, args.warmup)
     rows = rows_leg(args.steps)
     configs = {}
+    # The C5 and C3 lines are side figures: they take fixed samples (at least
+    # 100 timed steps after 50 warm-up steps, whatever --steps says) so that
+    # their per-step and per-kernel figures are stable; running right before
+    # the headline leg, they also leave the GPU at its sustained clocks when
+    # that leg's own --warmup and --steps begin.
     for name in ("C5", "C3"):
-        other = gpu_leg(args.steps, args.warmup, name=name, decode=False)
+        other = gpu_leg(max(args.steps, 100), max(args.warmup, 50), name=name, decode=False)
         configs[name] = {"workload": other["config"]["workload"],
                          "ms_per_step": other["ms_per_step"],
                          "useful_tflops": other["value"],
