@@ -218,7 +218,9 @@ __host__ __device__ inline PlanLayout plan_layout(int batch, int q_len, int kv_l
   p.kid = off;   off = align256(off + sizeof(int) * (size_t)batch * p.tk_pad);
   p.tmap = off;  off = align256(off + (size_t)batch * p.nq * p.nk);
   p.qcnt = off;  off = align256(off + sizeof(int) * (size_t)batch * p.nq);
-  // work lists of 64-row stages: [B][nq][2 nk] key stages, [B][nk][2 nq] query stages
+  // work lists of 64-row stages: [B][nq][2 nk] key stages, [B][nk][2 nq] query stages.
+  // The forward and dq read a query tile's list eight entries at a time and
+  // may read up to 7 entries past its end: a section must follow qlist.
   p.qlist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nq * 2 * p.nk);
   p.kcnt = off;  off = align256(off + sizeof(int) * (size_t)batch * p.nk);
   p.klist = off; off = align256(off + sizeof(int) * (size_t)batch * p.nk * 2 * p.nq);
