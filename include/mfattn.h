@@ -109,8 +109,10 @@ int mf_block_map_placements(const int32_t* placements, int count, int mode,
  * bidirectional.attention (kernels/bidirectional.py:7-35, modes 1 and 2).
  * Rows with no valid key (inactive queries) are written as exact zeros.
  * `scale` multiplies the logits (the reference uses head_dim ** -0.5,
- * attention.py:23-25).  `plan` must come from mf_block_map with the same
- * batch/q_len/kv_len and the mode the caller intends. */
+ * attention.py:23-25); it must be finite and positive in every attention
+ * and decode entry point (MF_ERR_INVALID_ARGUMENT otherwise).  `plan` must
+ * come from mf_block_map with the same batch/q_len/kv_len and the mode the
+ * caller intends. */
 int mf_attn_fwd(const void* q, const void* k, const void* v, int dtype,
                 int batch, int q_len, int kv_len, int q_heads, int kv_heads,
                 int head_dim, int mode, float scale, const void* plan,

@@ -2,6 +2,7 @@
 // launches.  Every check here runs on the host before anything is enqueued,
 // so a malformed call returns an MF_ERR_* code (and leaves a message for
 // mf_last_error) without touching the GPU.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -87,6 +88,15 @@ int check_hip(hipError_t e, const char* what) {
 int check_mode(int mode) {
   if (mode != MF_MODE_PACKED_CAUSAL && mode != MF_MODE_PACKED_BIDIR && mode != MF_MODE_KEYMASK_BIDIR)
     return fail(MF_ERR_MODE, "Unknown mask mode %d", mode);
+  return MF_OK;
+}
+
+// The logit scale: finite and positive (the reference scales by
+// head_dim ** -0.5, attention.py:23-25).  The forward takes each query's
+// running maximum on the raw scores and scales it once, which relies on it.
+int check_scale(float scale) {
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return fail(MF_ERR_INVALID_ARGUMENT, "scale must be finite and positive (got %g)", (double)scale);
   return MF_OK;
 }
 
@@ -189,6 +199,7 @@ int mf_attn_fwd(const void* q, const void* k, const void* v, int dtype, int batc
                 const void* plan, size_t plan_bytes, void* out, float* lse, void* stream) {
   if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
     return rc;
+  if (int rc = check_scale(scale)) return rc;
   if (!q || !k || !v || !plan || !out || !lse)
     return fail(MF_ERR_INVALID_ARGUMENT, "q, k, v, plan, out and lse must be non-null");
   return check_hip(mf::launch_attn_fwd(q, k, v, dtype == MF_DTYPE_F32, batch, q_len, kv_len,
@@ -213,6 +224,7 @@ int attn_bwd_phases(const void* q, const void* k, const void* v, const void* out
                     const char* what) {
   if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
     return rc;
+  if (int rc = check_scale(scale)) return rc;
   const bool need_qkv = phases & 6;
   if ((need_qkv && (!q || !k || !v || !plan)) || !lse || !dout || !workspace ||
       ((phases & 1) && !out) || ((phases & 2) && !dq) || ((phases & 4) && (!dk || !dv)))
@@ -312,6 +324,7 @@ int mf_decode_append(const void* q, const void* k_new, const void* v_new,
     return fail(MF_ERR_INVALID_ARGUMENT, "every tensor pointer and the workspace must be non-null");
   if (int rc = check_decode(dtype, batch, capacity, q_heads, kv_heads, head_dim, workspace_bytes))
     return rc;
+  if (int rc = check_scale(scale)) return rc;
   return check_hip(mf::launch_decode(q, k_cache, v_cache, nullptr, dtype == MF_DTYPE_F32, batch,
                                      capacity, q_heads, kv_heads, scale, out, workspace,
                                      static_cast<hipStream_t>(stream), k_new, v_new, positions),
@@ -326,6 +339,7 @@ int mf_decode(const void* q, const void* k_cache, const void* v_cache, const int
     return fail(MF_ERR_INVALID_ARGUMENT, "every tensor pointer and the workspace must be non-null");
   if (int rc = check_decode(dtype, batch, capacity, q_heads, kv_heads, head_dim, workspace_bytes))
     return rc;
+  if (int rc = check_scale(scale)) return rc;
   return check_hip(mf::launch_decode(q, k_cache, v_cache, lengths, dtype == MF_DTYPE_F32, batch,
                                      capacity, q_heads, kv_heads, scale, out, workspace,
                                      static_cast<hipStream_t>(stream)),
@@ -380,6 +394,7 @@ int mf_attn_fwd_rope_q(const void* q_raw, const void* k, const void* v, const vo
   if (int rc = check_attn(dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, mode, plan_bytes))
     return rc;
   if (int rc = check_rope(dtype, batch, q_len, q_heads, kv_heads, head_dim, rope_theta)) return rc;
+  if (int rc = check_scale(scale)) return rc;
   if (dtype != MF_DTYPE_BF16)
     return fail(MF_ERR_DTYPE, "mf_attn_fwd_rope_q serves bf16 tensors (dtype code %d)", dtype);
   if (!q_raw || !k || !v || !q_gain || !plan || !table || !out || !lse)
@@ -517,6 +532,8 @@ int abi_fail(int code, const char* fmt, ...) {
 }
 
 int abi_check_hip(hipError_t e, const char* what) { return check_hip(e, what); }
+
+int abi_check_scale(float scale) { return check_scale(scale); }
 
 int abi_check_decode_shape(int dtype, int batch, int capacity, int q_heads, int kv_heads,
                            int head_dim) {

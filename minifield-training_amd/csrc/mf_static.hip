@@ -24,6 +24,7 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const int3
                          const void* v_new, const int32_t* positions);
 int abi_fail(int code, const char* fmt, ...);
 int abi_check_hip(hipError_t e, const char* what);
+int abi_check_scale(float scale);
 int abi_check_decode_shape(int dtype, int batch, int capacity, int q_heads, int kv_heads,
                            int head_dim);
 }  // namespace mf
@@ -71,6 +72,7 @@ int mf_decode_static(const void* q, const void* k_cache, const void* v_cache,
                      int kv_heads, int head_dim, float scale, void* out, void* stream) {
   if (int rc = mf::abi_check_decode_shape(dtype, batch, capacity, q_heads, kv_heads, head_dim))
     return rc;
+  if (int rc = mf::abi_check_scale(scale)) return rc;
   const bool f32 = dtype == MF_DTYPE_F32;
   const size_t need = mf::decode_workspace_bytes_any(batch, capacity, q_heads);
   if (need > kScratchBytes)

@@ -67,6 +67,11 @@ def _msg():
         # the kernels' 32-bit DMA offsets cover one batch row of q and of k/v
         (dict(t=1 << 20, s=1 << 20, hq=16, hkv=8), _lib.ERR_SHAPE, "exceeds 4 GiB"),
         (dict(), _lib.ERR_INVALID_ARGUMENT, "non-null"),
+        # the reference scales by head_dim ** -0.5; the forward's running max relies on scale > 0
+        (dict(scale=0.0), _lib.ERR_INVALID_ARGUMENT, "scale must be finite and positive"),
+        (dict(scale=-0.125), _lib.ERR_INVALID_ARGUMENT, "scale must be finite and positive"),
+        (dict(scale=float("nan")), _lib.ERR_INVALID_ARGUMENT, "scale must be finite and positive"),
+        (dict(scale=float("inf")), _lib.ERR_INVALID_ARGUMENT, "scale must be finite and positive"),
     ],
 )
 def test_forward_rejects_bad_arguments_on_the_host(kw, code, text):
@@ -98,6 +103,34 @@ def test_block_map_and_decode_reject_bad_arguments():
         _lib.ERR_INVALID_ARGUMENT
     assert L.mf_attn_bwd_workspace_bytes(2, 6, 4) == 2 * 2 * 6 * 4 * 4
     assert L.mf_decode_workspace_bytes(64, 8192, 16, 64) > 0
+
+
+@pytest.mark.parametrize("scale", [0.0, -1.0, float("nan"), float("-inf")])
+def test_every_attention_entry_point_refuses_a_bad_scale(scale):
+    L = _lib.LIB
+    buf = ctypes.create_string_buffer(64)  # non-null host addresses: checks fail before launch
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    big = 1 << 40
+    calls = {
+        "mf_attn_bwd": lambda: L.mf_attn_bwd(p, p, p, p, p, p, _lib.DTYPE_BF16, 1, 8, 8, 4, 2, 64, 0,
+                                             scale, p, big, p, p, p, p, big, None),
+        "mf_attn_bwd_dq": lambda: L.mf_attn_bwd_dq(p, p, p, p, p, _lib.DTYPE_BF16, 1, 8, 8, 4, 2, 64,
+                                                   0, scale, p, big, p, p, big, None),
+        "mf_attn_bwd_dkdv": lambda: L.mf_attn_bwd_dkdv(p, p, p, p, p, _lib.DTYPE_BF16, 1, 8, 8, 4, 2,
+                                                       64, 0, scale, p, big, p, p, p, big, None),
+        "mf_decode": lambda: L.mf_decode(p, p, p, p, _lib.DTYPE_BF16, 2, 6, 4, 2, 64, scale, p, p,
+                                         big, None),
+        "mf_decode_append": lambda: L.mf_decode_append(p, p, p, p, _lib.DTYPE_BF16, 2, 6, 4, 2, 64,
+                                                       scale, p, p, p, p, big, None),
+        "mf_decode_static": lambda: L.mf_decode_static(p, p, p, p, _lib.DTYPE_BF16, 2, 6, 4, 2, 64,
+                                                       scale, p, None),
+        "mf_attn_fwd_rope_q": lambda: L.mf_attn_fwd_rope_q(p, p, p, p, None, _lib.DTYPE_BF16, 2, 8, 8,
+                                                           4, 2, 64, 0, scale, 1e-6, 10000.0, p, big,
+                                                           p, big, p, p, None),
+    }
+    for name, call in calls.items():
+        assert call() == _lib.ERR_INVALID_ARGUMENT, name
+        assert "scale must be finite and positive" in _msg(), name
 
 
 def test_decode_append_rejects_bad_arguments():
