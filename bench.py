@@ -29,8 +29,10 @@
   mean segment 512) and C5 (1 x 32768, segments of 16-128 tokens): ms per
   step, useful TFLOP/s and the fraction of the max(MFMA, HBM) roofline time.
 
-The decode, the rows, C5 and then C3 are measured before the C2 step, so the
-GPU's clocks are near their steady state when the headline is timed.
+The decode, the rows, C5 and then C3 are measured before the C2 step.  Each
+packed leg first runs ``SETTLE_STEPS`` untimed steps of its own workload (the
+GPU's clocks take ~30 launches to settle after a change of load), then its
+per-kernel sample, then its ``--warmup`` and ``--steps``.
 ``--config C3`` or ``--config C5`` (or ``--config C2 --step-only``) prints one of
 those step lines alone.
 
@@ -53,6 +55,8 @@ sys.path.insert(0, str(ROOT))
 METRIC = "packed GQA attn fwd+bwd useful TFLOP/s @350M shape; ragged decode HBM GB/s"
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 HBM_PEAK_GBPS = 8000.0
+# untimed steps of a packed leg's workload before its measurements (clock settling)
+SETTLE_STEPS = 40
 
 
 def _events(n):
@@ -122,6 +126,44 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False, name: str = "C2", de
         torch.cuda.empty_cache()
         decode_leg(0, 0, profile=True)
         return None
+
+    # Clock settling: after a switch from another workload (or from idle) the
+    # step runs ~13 % slower for its first ~30 launches while the GPU's clocks
+    # settle on the new load (one box, per-step times: ~700 us at steps 4-9,
+    # ~615 us from step 35 on), which a 5-step warm-up leaves inside a 20-step
+    # timed window.  SETTLE_STEPS untimed steps of this workload (~25 ms at C2)
+    # come before any of this leg's measurements.
+    for _ in range(SETTLE_STEPS):
+        step()
+    torch.cuda.synchronize()
+
+    # Per-kernel durations: HIP events on the launch stream between the
+    # launches of a step, over a fixed sample of at least 50 steps of this
+    # workload.  The backward is the product call (dq with D fused in, then
+    # dk/dv); dk/dv is then launched once more on its own through its phase
+    # entry point (same kernel, D from an untimed delta launch), and dq is the
+    # difference.
+    names = ("block_map", "attn_fwd", "attn_bwd", "attn_bwd_dkdv")
+    out, lse = ops.attn_fwd(q, k, v, ops.block_map(seg, mask, mode, w.length, w.length), mode, scale)
+    ops.attn_bwd_delta(out, do, lse, ws)
+    samples = max(steps, 50)
+    marks = [_events(len(names) + 1) for _ in range(samples)]
+    for ev in marks:
+        ev[0].record()
+        plan = ops.block_map(seg, mask, mode, w.length, w.length)
+        ev[1].record()
+        out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
+        ev[2].record()
+        ops.attn_bwd(q, k, v, out, do, lse, plan, mode, scale)
+        ev[3].record()
+        ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv)
+        ev[4].record()
+    torch.cuda.synchronize()
+    kern = {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in marks) / samples
+            for i, name in enumerate(names)}
+    kern["attn_bwd_dq"] = kern["attn_bwd"] - kern["attn_bwd_dkdv"]
+
+    # the product step: `warmup` untimed steps, then exactly `steps` timed ones
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -134,31 +176,6 @@ def gpu_leg(steps: int, warmup: int, profile: bool = False, name: str = "C2", de
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     ms = start.elapsed_time(end) / steps
-
-    # per-kernel durations: HIP events on the launch stream between the
-    # launches of a step, over as many steps as were timed, so every kernel
-    # runs in the same order and cache state as in the timed loop.  The
-    # backward is the product call (dq with D fused in, then dk/dv); dk/dv is
-    # then launched once more on its own through its phase entry point (same
-    # kernel, D from an untimed delta launch), and dq is the difference.
-    names = ("block_map", "attn_fwd", "attn_bwd", "attn_bwd_dkdv")
-    out, lse = ops.attn_fwd(q, k, v, ops.block_map(seg, mask, mode, w.length, w.length), mode, scale)
-    ops.attn_bwd_delta(out, do, lse, ws)
-    marks = [_events(len(names) + 1) for _ in range(steps)]
-    for ev in marks:
-        ev[0].record()
-        plan = ops.block_map(seg, mask, mode, w.length, w.length)
-        ev[1].record()
-        out, lse = ops.attn_fwd(q, k, v, plan, mode, scale)
-        ev[2].record()
-        ops.attn_bwd(q, k, v, out, do, lse, plan, mode, scale)
-        ev[3].record()
-        ops.attn_bwd_dkdv(q, k, v, do, lse, plan, mode, scale, ws, dk, dv)
-        ev[4].record()
-    torch.cuda.synchronize()
-    kern = {name: sum(ev[i].elapsed_time(ev[i + 1]) for ev in marks) / steps
-            for i, name in enumerate(names)}
-    kern["attn_bwd_dq"] = kern["attn_bwd"] - kern["attn_bwd_dkdv"]
     flops = workloads.attention_flops(w)
     nbytes = workloads.attention_bytes(w)["fwd_bwd"]
     algo = {"attn_fwd": flops["fwd"], "attn_bwd_dq": flops["dq"], "attn_bwd_dkdv": flops["dkdv"]}
@@ -592,19 +609,16 @@ def main() -> int:
                           "step_roofline_frac": gpu["step_roofline_frac"],
                           "step_roofline": gpu["step_roofline"]}))
         return 0
-    # The other measurements run first: their GPU work also brings the clocks to
-    # their steady state before the headline C2 step is timed.  C3, the heaviest
-    # of them, runs last: after a lighter load the C2 step slows for its first
-    # ~30 steps while the clocks settle (one box, per-step times: ~700 us at steps
-    # 4-9, ~615 us from step 35), less so right after C3.
+    # The other measurements run first, the headline C2 leg last; each packed
+    # leg measures its per-kernel sample before its own warm-up and timed steps
+    # (gpu_leg), so every timed window starts with the clocks settled on its
+    # workload.
     decode = decode_leg(args.steps, args.warmup)
     rows = rows_leg(args.steps)
     configs = {}
     # The C5 and C3 lines are side figures: they take fixed samples (at least
     # 100 timed steps after 50 warm-up steps, whatever --steps says) so that
-    # their per-step and per-kernel figures are stable; running right before
-    # the headline leg, they also leave the GPU at its sustained clocks when
-    # that leg's own --warmup and --steps begin.
+    # their per-step and per-kernel figures are stable.
     for name in ("C5", "C3"):
         other = gpu_leg(max(args.steps, 100), max(args.warmup, 50), name=name, decode=False)
         configs[name] = {"workload": other["config"]["workload"],
