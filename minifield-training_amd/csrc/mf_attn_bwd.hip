@@ -650,6 +650,7 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   drain_memory();
   lse2 = qactive ? lse_raw * kLog2e : kPosInf;
   dlt = qactive ? dlt_raw : 0.f;
+  // (a slot past the end is skipped whole, as in the forward)
   for (int i = 0; i < nslots; i += 2) {
     const i32x8u e = ld_const8(list, 2 * i);
     wait_vmcnt<0>();
@@ -657,11 +658,13 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
     if (i > 0) issue_slot(i + 1, e[2], e[3], slotB);
     compute(e[0], slotA);
     if (2 * i + 1 < nsteps) compute(e[1], slotA + kStageBytes);
-    wait_vmcnt<0>();
-    barrier();
-    issue_slot(i + 2, e[4], e[5], slotA);
-    if (2 * i + 2 < nsteps) compute(e[2], slotB);
-    if (2 * i + 3 < nsteps) compute(e[3], slotB + kStageBytes);
+    if (i + 1 < nslots) {
+      wait_vmcnt<0>();
+      barrier();
+      issue_slot(i + 2, e[4], e[5], slotA);
+      compute(e[2], slotB);
+      if (2 * i + 3 < nsteps) compute(e[3], slotB + kStageBytes);
+    }
   }
   wait_vmcnt<0>();
 
@@ -921,7 +924,9 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
   // accumulators three exit paths, resolved with 64-register copies).  Waves
   // below kWordArrays issue one more DMA per step than the others; the step
   // wait uses the tile count, which for them also covers the oldest DMA of
-  // the stage issued one step earlier.
+  // the stage issued one step earlier.  (Skipping the steps past the end
+  // whole -- their waits, barriers and clamped re-issues of the last stage --
+  // measured 1.7-2.2% slower at C2 and within 1% at C3 and C5.)
   constexpr int G = Q::kGroupsPerWave;
   if (niters > 0) {
     issue(0, stage0);

@@ -556,7 +556,8 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     const i32x8u e = ld_const8(list, 0);
     issue_slot(0, e[0], e[1], slotA);
   }
-  // Whole pairs of slots; the computes past the end are skipped rather than
+  // Whole pairs of slots; a slot past the end is skipped whole (its wait,
+  // barrier and computes; nslots is uniform over the workgroup) rather than
   // leaving the loop mid-pair (a mid-pair exit gives the accumulators two
   // exit paths, resolved with register copies).
   for (int i = 0; i < nslots; i += 2) {
@@ -566,11 +567,13 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
     issue_slot(i + 1, e[2], e[3], slotB);
     compute(2 * i, e[0], slotA);
     if (2 * i + 1 < nsteps) compute(2 * i + 1, e[1], slotA + kStageBytes);
-    wait_vmcnt<0>();
-    barrier();
-    issue_slot(i + 2, e[4], e[5], slotA);
-    if (2 * i + 2 < nsteps) compute(2 * i + 2, e[2], slotB);
-    if (2 * i + 3 < nsteps) compute(2 * i + 3, e[3], slotB + kStageBytes);
+    if (i + 1 < nslots) {
+      wait_vmcnt<0>();
+      barrier();
+      issue_slot(i + 2, e[4], e[5], slotA);
+      compute(2 * i + 2, e[2], slotB);
+      if (2 * i + 3 < nsteps) compute(2 * i + 3, e[3], slotB + kStageBytes);
+    }
   }
   wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 
