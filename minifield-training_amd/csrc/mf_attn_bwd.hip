@@ -505,6 +505,7 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
 
   bf16x8 qf[4], gf[4];  // query and output-gradient fragments (loaded below)
   float lse2 = 0.f, dlt = 0.f;
+  uint64_t ndlt2 = 0;  // (-D, -D) of the lane's row, the start of each dP^T block
   f32x16 dqacc[2] = {zero16(), zero16()};
   const float c = a.scale_log2;
 
@@ -533,7 +534,29 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
 
   auto block = [&](const char* kt, const char* vt, const int* kids_lds, int kb, int kb2,
                    bool mask_ids, bool diag) {
-    f32x16 s = zero16(), dp = zero16();
+    f32x16 s = zero16();
+    f32x16 dp;
+    {
+      // dP^T starts from -D (per lane: one query row), so the MFMA chain
+      // yields dP - D and the 16 subtractions per block go: eight 64-bit
+      // moves of the lane's (-D, -D) pair, in asm because the compiler either
+      // hoists a sixteen-register splat out of the loop (spilling at 128
+      // VGPRs) or emits sixteen 32-bit moves.  s_nop 1 gives the two wait
+      // states between a VALU write and an MFMA reading it as SrcC.  The
+      // registers written are the block's dP accumulators, which no MFMA in
+      // flight reads as SrcC (the previous block's dP chain finished before
+      // its probabilities were formed).
+      uint64_t p0, p1, p2, p3, p4, p5, p6, p7;
+      asm volatile(
+          "v_mov_b64 %0, %8\n\tv_mov_b64 %1, %8\n\tv_mov_b64 %2, %8\n\tv_mov_b64 %3, %8\n\t"
+          "v_mov_b64 %4, %8\n\tv_mov_b64 %5, %8\n\tv_mov_b64 %6, %8\n\tv_mov_b64 %7, %8\n\t"
+          "s_nop 1"
+          : "=&v"(p0), "=&v"(p1), "=&v"(p2), "=&v"(p3), "=&v"(p4), "=&v"(p5), "=&v"(p6),
+            "=&v"(p7)
+          : "v"(ndlt2));
+      typedef uint64_t u64x8 __attribute__((ext_vector_type(8)));
+      dp = __builtin_bit_cast(f32x16, (u64x8){p0, p1, p2, p3, p4, p5, p6, p7});
+    }
     const int krow = kb2 * 32 + (lane & 31);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -555,7 +578,7 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
         s[r] = kb + kb2 * 32 + acc_row(r, lane) <= qpos ? s[r] : kNegInf;
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], c, -lse2)) * (dp[r] - dlt);
+    for (int r = 0; r < 16; ++r) s[r] = fast_exp2(fmaf(s[r], c, -lse2)) * dp[r];
     const bf16x8 ds0 = pack8(s, 0), ds1 = pack8(s, 8);
 #pragma unroll
     for (int db = 0; db < 2; ++db) {
@@ -650,6 +673,10 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   drain_memory();
   lse2 = qactive ? lse_raw * kLog2e : kPosInf;
   dlt = qactive ? dlt_raw : 0.f;
+  {
+    const uint32_t nd = __builtin_bit_cast(uint32_t, -dlt);
+    ndlt2 = ((uint64_t)nd << 32) | nd;
+  }
   // (a slot past the end is skipped whole, as in the forward)
   for (int i = 0; i < nslots; i += 2) {
     const i32x8u e = ld_const8(list, 2 * i);
