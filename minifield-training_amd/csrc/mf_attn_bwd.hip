@@ -715,9 +715,7 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d0 = db * 32 + 8 * g4 + 4 * ehalf;
-      bf16x4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = (bf16)(qactive ? dqacc[db][g4 * 4 + i] * a.scale : 0.f);
+      const bf16x4 o = scaled_bf16x4(dqacc[db], g4 * 4, a.scale, qactive);
       *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dq) +
                                  (((size_t)b * a.T + eqpos) * a.Hq + head) * kD + d0) = o;
     }
@@ -983,12 +981,8 @@ void bwd_dkdv_bf16_kernel(BwdArgs a) {
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d0 = db * 32 + 8 * g4 + 4 * half;
       const size_t off = (((size_t)b * a.S + kpos) * a.Hkv + kvh) * kD + d0;
-      bf16x4 ok, ov;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ok[i] = (bf16)(kactive ? dkacc[db][g4 * 4 + i] * a.scale : 0.f);
-        ov[i] = (bf16)(kactive ? dvacc[db][g4 * 4 + i] : 0.f);
-      }
+      const bf16x4 ok = scaled_bf16x4(dkacc[db], g4 * 4, a.scale, kactive);
+      const bf16x4 ov = scaled_bf16x4(dvacc[db], g4 * 4, 1.f, kactive);
       *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dk) + off) = ok;
       *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.dv) + off) = ov;
     }

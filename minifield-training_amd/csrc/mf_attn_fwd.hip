@@ -597,9 +597,7 @@ void attn_fwd_bf16_kernel(FwdArgs a) {
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
         const int d0 = db * 32 + 8 * g4 + 4 * ehalf;
-        bf16x4 o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (bf16)(has ? oacc[db][g4 * 4 + i] * inv : 0.f);
+        const bf16x4 o = scaled_bf16x4(oacc[db], g4 * 4, inv, has);
         *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.out) +
                                    (((size_t)b * a.T + eqpos) * a.Hq + head) * kD + d0) = o;
       }

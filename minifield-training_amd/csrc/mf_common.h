@@ -112,6 +112,21 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& v, int base) {
   return o;
 }
 
+// Four accumulator values times `mul` as bf16 (round to nearest even), or
+// zeros where `keep` is false.  The select acts on the two packed words, not
+// on each value, so the conversions pair up (one v_cvt_pk_bf16_f32 per two
+// values and no repacking): a select per value before the cast makes the
+// compiler convert one value at a time and merge the halves afterwards.
+__device__ __forceinline__ bf16x4 scaled_bf16x4(const f32x16& v, int base, float mul, bool keep) {
+  bf16x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (bf16)(v[base + i] * mul);
+  u32x2 w = __builtin_bit_cast(u32x2, o);
+  w[0] = keep ? w[0] : 0u;
+  w[1] = keep ? w[1] : 0u;
+  return __builtin_bit_cast(bf16x4, w);
+}
+
 __device__ __forceinline__ bf16x8 ld_bf16x8(const void* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
