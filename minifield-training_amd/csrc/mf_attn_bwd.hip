@@ -519,8 +519,9 @@ void bwd_dq_bf16_kernel(BwdArgs a) {
   const char* kg = reinterpret_cast<const char*>(a.k) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
   const char* vg = reinterpret_cast<const char*>(a.v) + ((size_t)b * a.S * a.Hkv + kvh) * kD * sizeof(bf16);
 
-  // (the precomputed-offset form of kv_dma measured 2-5% slower here: its
-  // offsets cost dq registers that it then spills)
+  // (the precomputed-offset form of kv_dma measured 2-5% slower here while
+  // its offsets made dq spill; without spills, at 128 VGPRs, it measures
+  // within 0.6%)
   auto issue = [&](int entry, char* stage) {
     kv_dma<W>(kg, vg, row_stride, a.S, kid_row, (entry >> 2) * kKvStep, wave, stage);
   };
